@@ -1,0 +1,132 @@
+"""In-tree build of the gfx950 library and its PyTorch registration module.
+
+Produces, inside ``flash_hypercons/``:
+
+* ``libflash_hypercons_hip.so`` -- every HIP kernel plus the C ABI declared in
+  ``include/flash_hypercons.h`` (hipcc, ``--offload-arch=gfx950`` only);
+* ``_C.so`` -- the CPython/PyTorch module that registers the
+  ``flash_hypercons::*`` operators and calls the C ABI (host-only C++).
+
+Run ``python flash-hyperconnections_amd/build.py`` (or ``__graft_entry__.build()``).
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+import sysconfig
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parent
+CSRC = HERE / "csrc"
+PKG = HERE / "flash_hypercons"
+INCLUDE = ROOT / "include"
+OBJ = HERE / "_build"
+ARCH = "gfx950"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+HIPCC = str(ROCM / "bin" / "hipcc")
+
+LIB_NAME = "libflash_hypercons_hip.so"
+KERNEL_SOURCES = [
+    "expm_generic.hip",
+    "expm_quad.hip",
+    "expm_oct.hip",
+    "expm_tile.hip",
+    "expm_params.hip",
+    "fh_capi.cpp",
+]
+
+# -ffp-contract=off: every fused multiply-add in the kernels is written out.
+# The packed-FP32 feature is switched off (v_pk_*_f32 stay out of the code).
+HIP_FLAGS = [
+    "-x", "hip",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    f"--offload-arch={ARCH}",
+    "-ffp-contract=off",
+    "-fno-gpu-flush-denormals-to-zero",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-fvisibility=hidden",
+    "-Wall",
+    f"-I{INCLUDE}",
+    f"-I{CSRC}",
+]
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(
+        line for line in proc.stdout.splitlines()
+        if "packed-fp32-ops" not in line or "warning" not in line
+    )
+    if proc.returncode != 0:
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
+
+
+def _compile(src: str) -> Path:
+    obj = OBJ / (src + ".o")
+    _run([HIPCC, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+    return obj
+
+
+def build_library(jobs: int = 8) -> Path:
+    OBJ.mkdir(exist_ok=True)
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        objs = list(pool.map(_compile, KERNEL_SOURCES))
+    target = PKG / LIB_NAME
+    tmp = target.with_suffix(".so.tmp")
+    _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(tmp)])
+    os.replace(tmp, target)
+    return target
+
+
+def build_extension() -> Path:
+    import torch
+    from torch.utils.cpp_extension import include_paths, library_paths
+
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    torch_lib = library_paths()[0]
+    flags = [
+        "-O2", "-std=c++17", "-fPIC", "-fvisibility=hidden",
+        "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+        "-DTORCH_EXTENSION_NAME=_C", "-DTORCH_API_INCLUDE_EXTENSION_H",
+        *[f"-I{p}" for p in include_paths()],
+        f"-I{sysconfig.get_paths()['include']}",
+        f"-I{ROCM / 'include'}",
+        f"-I{INCLUDE}",
+    ]
+    OBJ.mkdir(exist_ok=True)
+    obj = OBJ / "register.o"
+    cxx = shutil.which("g++") or "g++"
+    _run([cxx, *flags, "-c", str(CSRC / "register.cpp"), "-o", str(obj)])
+    target = PKG / "_C.so"
+    tmp = target.with_suffix(".so.tmp")
+    _run([
+        cxx, "-shared", str(obj), "-o", str(tmp),
+        f"-L{PKG}", "-l:" + LIB_NAME,
+        f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-ltorch_python",
+        f"-L{ROCM / 'lib'}", "-lamdhip64",
+        "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}", f"-Wl,-rpath,{ROCM / 'lib'}",
+    ])
+    os.replace(tmp, target)
+    return target
+
+
+def build(jobs: int = 8) -> list[Path]:
+    lib = build_library(jobs)
+    ext = build_extension()
+    return [lib, ext]
+
+
+def built() -> bool:
+    return (PKG / LIB_NAME).exists() and (PKG / "_C.so").exists()
+
+
+if __name__ == "__main__":
+    for path in build(int(sys.argv[1]) if len(sys.argv) > 1 else 8):
+        print(path)

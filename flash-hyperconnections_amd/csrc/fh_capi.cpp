@@ -1,0 +1,150 @@
+// C-ABI entry points of libflash_hypercons_hip.so (declared in
+// include/flash_hypercons.h): argument validation, operand description and
+// kernel selection.  Replaces the reference's host launcher
+// csrc/matrix_exp.cu:13-86 without its FP32/contiguous/padded staging copies:
+// the kernels read the caller's strided storage directly and write only the
+// logical n x n block.
+#include <string>
+
+#include "fh_kernels.h"
+#include "flash_hypercons.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+// The reference's input check message (csrc/matrix_exp.cu:52-55).
+constexpr const char* kInputMessage =
+    "expected a strided CUDA [B, N, N] tensor, 2 <= N <= 32, in float32, float16, or bfloat16";
+constexpr const char* kDirectionMessage = "matrix exponential direction must match the input";
+
+int fail(int code, const std::string& message) {
+  g_error = message;
+  return code;
+}
+
+int element_size(int dtype) { return dtype == FH_DTYPE_F32 ? 4 : 2; }
+
+bool aligned(const void* p, int64_t bytes) {
+  return (reinterpret_cast<uintptr_t>(p) % static_cast<uintptr_t>(bytes)) == 0;
+}
+
+fh::Operand make_operand(const void* data, const int64_t strides[3], int neg, int dtype, int n) {
+  fh::Operand op;
+  op.data = data;
+  op.sb = strides[0];
+  op.sr = strides[1];
+  op.sc = strides[2];
+  op.sign = neg ? -1.f : 1.f;
+  op.vec = fh::kVecNone;
+  if (n == 4) {
+    // A whole row (or column) of the 4 x 4 matrix is one aligned vector when
+    // its elements are adjacent and every matrix/row (column) start keeps the
+    // vector alignment.
+    const int64_t vbytes = 4 * element_size(dtype);
+    const bool base_ok = aligned(data, vbytes) && strides[0] % 4 == 0;
+    if (base_ok && strides[2] == 1 && strides[1] % 4 == 0) {
+      op.vec = fh::kVecRows;
+    } else if (base_ok && strides[1] == 1 && strides[2] % 4 == 0) {
+      op.vec = fh::kVecCols;
+    }
+  }
+  return op;
+}
+
+int validate(const void* input, const int64_t* strides, int dtype, int64_t batch, int n, const void* out) {
+  if (n < 2 || n > 32 || (dtype != FH_DTYPE_F32 && dtype != FH_DTYPE_BF16 && dtype != FH_DTYPE_F16) || batch < 0)
+    return fail(FH_ERR_INVALID_ARGUMENT, kInputMessage);
+  if (batch > 0 && (input == nullptr || strides == nullptr || out == nullptr))
+    return fail(FH_ERR_INVALID_ARGUMENT, "null input, stride or output pointer");
+  return FH_OK;
+}
+
+int launch(const void* input, const int64_t input_strides[3], int input_neg, const void* direction,
+           const int64_t direction_strides[3], int direction_neg, void* out, int dtype, int64_t batch, int n,
+           int variant, int32_t* s_out, hipStream_t stream) {
+  int rc = validate(input, input_strides, dtype, batch, n, out);
+  if (rc != FH_OK) return rc;
+  if (variant != FH_VARIANT_AUTO && variant != FH_VARIANT_GENERIC)
+    return fail(FH_ERR_INVALID_ARGUMENT, "unknown kernel variant");
+  const bool pair = direction != nullptr;
+  if (pair && batch > 0 && direction_strides == nullptr) return fail(FH_ERR_INVALID_ARGUMENT, kDirectionMessage);
+  if (batch == 0) return FH_OK;  // csrc/matrix_exp.cu:62-64
+  fh::ExpmArgs args;
+  args.x = make_operand(input, input_strides, input_neg, dtype, n);
+  if (pair) {
+    args.g = make_operand(direction, direction_strides, direction_neg, dtype, n);
+  } else {
+    args.g = args.x;
+  }
+  args.out = out;
+  args.s_out = s_out;
+  args.batch = batch;
+  args.n = n;
+  const int P = n <= 4 ? 4 : n <= 8 ? 8 : n <= 16 ? 16 : 32;  // csrc/matrix_exp.cu:65
+  hipError_t err;
+  if (variant == FH_VARIANT_GENERIC) {
+    err = fh::launch_generic(args, dtype, P, pair, stream);
+  } else if (P == 4) {
+    err = fh::launch_quad(args, dtype, pair, stream);
+  } else if (P == 8) {
+    err = fh::launch_oct(args, dtype, pair, stream);
+  } else {
+    err = fh::launch_tile(args, dtype, P, pair, stream);
+  }
+  if (err != hipSuccess) return fail(FH_ERR_LAUNCH, std::string("kernel launch failed: ") + hipGetErrorString(err));
+  g_error.clear();
+  return FH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fh_matrix_exp(const void* input, const int64_t strides[3], int input_neg, void* out, int dtype, int64_t batch,
+                  int n, hipStream_t stream) {
+  return launch(input, strides, input_neg, nullptr, nullptr, 0, out, dtype, batch, n, FH_VARIANT_AUTO, nullptr,
+                stream);
+}
+
+int fh_frechet(const void* input, const int64_t input_strides[3], int input_neg, const void* direction,
+               const int64_t direction_strides[3], int direction_neg, void* out, int dtype, int64_t batch, int n,
+               hipStream_t stream) {
+  if (batch > 0 && direction == nullptr) return fail(FH_ERR_INVALID_ARGUMENT, kDirectionMessage);
+  return launch(input, input_strides, input_neg, direction, direction_strides, direction_neg, out, dtype, batch, n,
+                FH_VARIANT_AUTO, nullptr, stream);
+}
+
+int fh_expm_launch(const void* input, const int64_t input_strides[3], int input_neg, const void* direction,
+                   const int64_t direction_strides[3], int direction_neg, void* out, int dtype, int64_t batch, int n,
+                   int variant, int32_t* s_out, hipStream_t stream) {
+  return launch(input, input_strides, input_neg, direction, direction_strides, direction_neg, out, dtype, batch, n,
+                variant, s_out, stream);
+}
+
+int fh_expm_params(const void* input, const int64_t input_strides[3], int input_neg, const void* direction,
+                   const int64_t direction_strides[3], int direction_neg, int dtype, int64_t batch, int n,
+                   int32_t* params, double* norms, hipStream_t stream) {
+  int rc = validate(input, input_strides, dtype, batch, n, params);
+  if (rc != FH_OK) return rc;
+  const bool pair = direction != nullptr;
+  if (pair && batch > 0 && direction_strides == nullptr) return fail(FH_ERR_INVALID_ARGUMENT, kDirectionMessage);
+  if (batch == 0) return FH_OK;
+  fh::ExpmArgs args;
+  args.x = make_operand(input, input_strides, input_neg, dtype, n);
+  args.g = pair ? make_operand(direction, direction_strides, direction_neg, dtype, n) : args.x;
+  args.out = nullptr;
+  args.s_out = nullptr;
+  args.batch = batch;
+  args.n = n;
+  const hipError_t err = fh::launch_params(args, dtype, pair, params, norms, stream);
+  if (err != hipSuccess) return fail(FH_ERR_LAUNCH, std::string("kernel launch failed: ") + hipGetErrorString(err));
+  g_error.clear();
+  return FH_OK;
+}
+
+const char* fh_last_error(void) { return g_error.c_str(); }
+
+const char* fh_version(void) { return "0.1.0"; }
+
+}  // extern "C"

@@ -1,0 +1,127 @@
+// Shared device-side pieces of the gfx950 small-matrix exponential kernels:
+// kernel argument block, element load/store with exact dtype conversion, the
+// degree-18 coefficient table and the squaring-count rule.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fh {
+
+// Squaring threshold of the degree-18 polynomial (reference
+// csrc/MatrixExpSmall.cuh:14).
+constexpr double kTheta18 = 3.010066362817634;
+
+// Coefficients of the Bader-Blanes-Casas (2019) degree-18 evaluation, as FP32
+// literals (reference csrc/MatrixExpSmall.cuh:89-103).  Row k is B(k+1);
+// columns multiply (I, A, A^2, A^3, A^6).
+#define FH_COEF_TABLE                                                                                   \
+  {                                                                                                     \
+    {0.f, -0.10036558103014462f, -0.008029246482411570f, -0.000892138498045730f, 0.f},                \
+    {0.f, 0.39784974949645076f, 1.36783778460411719f, 0.49828962252538268f,                            \
+     -0.00063789819459247233f},                                                                        \
+    {-10.96763960529620626f, 1.68015813878906197f, 0.05717798464788655f, -0.00698210122488052f,        \
+     3.349750170860705e-05f},                                                                          \
+    {-0.09043168323908106f, -0.06764045190713819f, 0.06759613017740597f, 0.02955525704293155f,         \
+     -1.391802575160607e-05f},                                                                         \
+    {0.f, 0.f, -0.09233646193671186f, -0.01693649390020817f, -1.400867981820361e-05f},                \
+  }
+
+__device__ constexpr float kCoef[5][5] = FH_COEF_TABLE;
+
+// Element types, tagged by the reference's dtype codes
+// (csrc/matrix_exp.cu:17: 0 = float32, 1 = bfloat16, 2 = float16).
+struct F32 {
+  using storage = float;
+  static constexpr int code = 0;
+};
+struct BF16 {
+  using storage = uint16_t;
+  static constexpr int code = 1;
+};
+struct F16 {
+  using storage = _Float16;
+  static constexpr int code = 2;
+};
+
+// One [batch, n, n] operand read through element strides.  `sign` is -1 for
+// a lazily negated tensor view and +1 otherwise (multiplying by it is exact).
+// `vec` tells the P == 4 kernel that whole rows (kVecRows: sc == 1) or whole
+// columns (kVecCols: sr == 1) of a 4 x 4 matrix are contiguous and aligned for
+// one vector load; the host sets it only when n == 4 and alignment holds.
+constexpr int kVecNone = 0;
+constexpr int kVecRows = 1;
+constexpr int kVecCols = 2;
+struct Operand {
+  const void* data;
+  int64_t sb, sr, sc;
+  float sign;
+  int vec;
+};
+
+struct ExpmArgs {
+  Operand x;        // the matrix X
+  Operand g;        // the Frechet direction G (unused by the forward)
+  void* out;        // contiguous [batch, n, n] in the input dtype
+  int32_t* s_out;   // optional per-matrix squaring count (-1: non-finite)
+  int64_t batch;
+  int n;
+};
+
+template <typename T>
+__device__ __forceinline__ float to_f32(typename T::storage v);
+template <>
+__device__ __forceinline__ float to_f32<F32>(float v) { return v; }
+template <>
+__device__ __forceinline__ float to_f32<F16>(_Float16 v) { return static_cast<float>(v); }
+template <>
+__device__ __forceinline__ float to_f32<BF16>(uint16_t v) {
+  return __uint_as_float(static_cast<uint32_t>(v) << 16);
+}
+
+// FP32 -> storage type, round to nearest even (the reference stores through
+// c10::BFloat16(float) / c10::Half(float), csrc/MatrixExpSmall.cuh:108-112).
+template <typename T>
+__device__ __forceinline__ typename T::storage from_f32(float v);
+template <>
+__device__ __forceinline__ float from_f32<F32>(float v) { return v; }
+template <>
+__device__ __forceinline__ _Float16 from_f32<F16>(float v) { return static_cast<_Float16>(v); }
+template <>
+__device__ __forceinline__ uint16_t from_f32<BF16>(float v) {
+  if (v != v) return 0x7FC0;
+  uint32_t u = __float_as_uint(v);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// Logical element (r, c) of matrix b, converted exactly to FP32.
+template <typename T>
+__device__ __forceinline__ float load_elem(const Operand& op, int64_t b, int r, int c) {
+  const auto* p = static_cast<const typename T::storage*>(op.data);
+  return to_f32<T>(p[b * op.sb + static_cast<int64_t>(r) * op.sr + static_cast<int64_t>(c) * op.sc]) * op.sign;
+}
+
+template <typename T>
+__device__ __forceinline__ void store_elem(void* out, int64_t idx, float v) {
+  static_cast<typename T::storage*>(out)[idx] = from_f32<T>(v);
+}
+
+// s = norm > theta18 ? ceil(log2(norm / theta18)) : 0, in double (reference
+// csrc/MatrixExpSmall.cuh:154, :356).  For q = norm/theta18 = m * 2^e with
+// m in [0.5, 1): ceil(log2 q) is e - 1 when m == 0.5 and e otherwise, and any
+// log2 accurate to better than 2^-40 relative returns the same integer ceiling
+// unless q lies within 2^-40 above a power of two; only that band calls log2.
+__device__ __forceinline__ int squarings_from_norm(double norm) {
+  if (!(norm > kTheta18)) return 0;
+  const double q = norm / kTheta18;
+  int e;
+  const double m = frexp(q, &e);
+  if (m == 0.5) return e - 1;
+  if (m < 0.5 + 0x1p-41) return static_cast<int>(ceil(log2(q)));
+  return e;
+}
+
+__device__ __forceinline__ bool finite_f32(float v) { return __builtin_isfinite(v); }
+
+}  // namespace fh

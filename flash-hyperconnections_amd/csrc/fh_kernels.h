@@ -1,0 +1,20 @@
+// Internal launcher declarations shared by the C-ABI entry points.
+#pragma once
+
+#include "fh_common.h"
+
+namespace fh {
+
+// One wavefront per matrix, reference evaluation order (checking aid).
+hipError_t launch_generic(const ExpmArgs& args, int dtype, int P, bool pair, hipStream_t stream);
+// P == 4: 16 matrices per wavefront on 4x4x1 MFMA.
+hipError_t launch_quad(const ExpmArgs& args, int dtype, bool pair, hipStream_t stream);
+// P == 8: 4 matrices per wavefront as 2x2 blocks of 4x4 MFMA tiles.
+hipError_t launch_oct(const ExpmArgs& args, int dtype, bool pair, hipStream_t stream);
+// P in {16, 32}: one wavefront per matrix on 16x16x4 / 32x32x2 MFMA.
+hipError_t launch_tile(const ExpmArgs& args, int dtype, int P, bool pair, hipStream_t stream);
+// (degree, s) and FP64 norm per matrix.
+hipError_t launch_params(const ExpmArgs& args, int dtype, bool pair, int32_t* params, double* norms,
+                         hipStream_t stream);
+
+}  // namespace fh

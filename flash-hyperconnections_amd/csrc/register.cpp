@@ -1,0 +1,137 @@
+// PyTorch-ROCm operator registration for flash_hypercons (the counterpart of
+// the reference's csrc/register.cpp and the ATen half of csrc/matrix_exp.cu).
+//
+// Schemas are the reference's (csrc/register.cpp:10-13) plus two debug ops.
+// The implementations sit on the CUDA dispatch key, which ROCm tensors use.
+// Each one checks its inputs with the reference's messages
+// (csrc/matrix_exp.cu:52-59), allocates the contiguous output in the input
+// dtype, and hands raw device pointers, element strides and the lazy-negation
+// bit to the C ABI of libflash_hypercons_hip.so on the current HIP stream.
+// No staging copies are made (the reference materialises FP32 contiguous
+// copies in prepare_matrix, csrc/matrix_exp.cu:35-44).
+#include <Python.h>
+
+#include <ATen/ATen.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+#include <torch/library.h>
+
+#include <optional>
+#include <tuple>
+
+#include "flash_hypercons.h"
+
+namespace flash_hypercons {
+namespace {
+
+int dtype_code(at::ScalarType t) {
+  return t == at::kFloat ? FH_DTYPE_F32 : t == at::kBFloat16 ? FH_DTYPE_BF16 : FH_DTYPE_F16;
+}
+
+void check_input(const at::Tensor& a) {
+  TORCH_CHECK(a.is_cuda() && a.layout() == at::kStrided && a.dim() == 3 && a.size(-1) == a.size(-2) &&
+                  a.size(-1) > 1 && a.size(-1) <= 32 &&
+                  (a.scalar_type() == at::kFloat || a.scalar_type() == at::kHalf ||
+                   a.scalar_type() == at::kBFloat16),
+              "expected a strided CUDA [B, N, N] tensor, 2 <= N <= 32, in float32, float16, or bfloat16");
+}
+
+void check_direction(const at::Tensor& a, const at::Tensor& d) {
+  TORCH_CHECK(d.sizes() == a.sizes() && d.device() == a.device() && d.scalar_type() == a.scalar_type() &&
+                  d.layout() == at::kStrided,
+              "matrix exponential direction must match the input");
+}
+
+struct View {
+  const void* data;
+  int64_t strides[3];
+  int neg;
+};
+
+View view_of(const at::Tensor& t) {
+  View v;
+  v.data = t.const_data_ptr();
+  v.strides[0] = t.stride(0);
+  v.strides[1] = t.stride(1);
+  v.strides[2] = t.stride(2);
+  v.neg = t.is_neg() ? 1 : 0;
+  return v;
+}
+
+hipStream_t current_stream() { return c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream(); }
+
+void check_status(int rc) { TORCH_CHECK(rc == FH_OK, "flash_hypercons: ", fh_last_error()); }
+
+at::Tensor run(const at::Tensor& a, const std::optional<at::Tensor>& direction, int variant, int32_t* s_out) {
+  check_input(a);
+  if (direction) check_direction(a, *direction);
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(a.device());
+  at::Tensor out = at::empty(a.sizes(), a.options());
+  if (a.numel() == 0) return out;
+  const View x = view_of(a);
+  const int n = static_cast<int>(a.size(-1));
+  if (direction) {
+    const View g = view_of(*direction);
+    check_status(fh_expm_launch(x.data, x.strides, x.neg, g.data, g.strides, g.neg, out.mutable_data_ptr(),
+                                dtype_code(a.scalar_type()), a.size(0), n, variant, s_out, current_stream()));
+  } else {
+    check_status(fh_expm_launch(x.data, x.strides, x.neg, nullptr, nullptr, 0, out.mutable_data_ptr(),
+                                dtype_code(a.scalar_type()), a.size(0), n, variant, s_out, current_stream()));
+  }
+  return out;
+}
+
+at::Tensor matrix_exp_hip(const at::Tensor& a) { return run(a, std::nullopt, FH_VARIANT_AUTO, nullptr); }
+
+at::Tensor frechet_hip(const at::Tensor& a, const at::Tensor& direction) {
+  return run(a, direction, FH_VARIANT_AUTO, nullptr);
+}
+
+// Debug: result of the chosen kernel family plus its per-matrix s.
+std::tuple<at::Tensor, at::Tensor> expm_debug_hip(const at::Tensor& a, const std::optional<at::Tensor>& direction,
+                                                  int64_t variant) {
+  check_input(a);
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(a.device());
+  at::Tensor s = at::empty({a.size(0)}, a.options().dtype(at::kInt));
+  at::Tensor out = run(a, direction, static_cast<int>(variant), s.mutable_data_ptr<int32_t>());
+  return {out, s};
+}
+
+// Debug: (degree, s) int32 [B, 2] and the FP64 norm [B] behind s.
+std::tuple<at::Tensor, at::Tensor> expm_params_hip(const at::Tensor& a, const std::optional<at::Tensor>& direction) {
+  check_input(a);
+  if (direction) check_direction(a, *direction);
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(a.device());
+  at::Tensor params = at::empty({a.size(0), 2}, a.options().dtype(at::kInt));
+  at::Tensor norms = at::empty({a.size(0)}, a.options().dtype(at::kDouble));
+  if (a.size(0) == 0) return {params, norms};
+  const View x = view_of(a);
+  const int n = static_cast<int>(a.size(-1));
+  View g{};
+  if (direction) g = view_of(*direction);
+  check_status(fh_expm_params(x.data, x.strides, x.neg, direction ? g.data : nullptr, direction ? g.strides : nullptr,
+                              g.neg, dtype_code(a.scalar_type()), a.size(0), n, params.mutable_data_ptr<int32_t>(),
+                              norms.mutable_data_ptr<double>(), current_stream()));
+  return {params, norms};
+}
+
+}  // namespace
+}  // namespace flash_hypercons
+
+TORCH_LIBRARY(flash_hypercons, m) {
+  m.def("_matrix_exp(Tensor input) -> Tensor");
+  m.def("_frechet(Tensor input, Tensor direction) -> Tensor");
+  m.def("_expm_debug(Tensor input, Tensor? direction, int variant) -> (Tensor, Tensor)");
+  m.def("_expm_params(Tensor input, Tensor? direction=None) -> (Tensor, Tensor)");
+}
+
+TORCH_LIBRARY_IMPL(flash_hypercons, CUDA, m) {
+  m.impl("_matrix_exp", &flash_hypercons::matrix_exp_hip);
+  m.impl("_frechet", &flash_hypercons::frechet_hip);
+  m.impl("_expm_debug", &flash_hypercons::expm_debug_hip);
+  m.impl("_expm_params", &flash_hypercons::expm_params_hip);
+}
+
+static PyModuleDef module = {PyModuleDef_HEAD_INIT, "_C", nullptr, -1, nullptr};
+
+PyMODINIT_FUNC PyInit__C() { return PyModule_Create(&module); }

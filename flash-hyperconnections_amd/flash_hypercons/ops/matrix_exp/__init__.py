@@ -1,0 +1,159 @@
+"""Adaptive small-matrix exponentials and scoped PyTorch routing (MI355X / gfx950).
+
+Python surface of the reference's ``flash_hypercons/ops/matrix_exp/__init__.py``
+(same names, routing rules and error behaviour).  Eligible tensors -- strided
+``[B, N, N]`` ROCm tensors on a gfx950 device with 2 <= N <= 32 in float32,
+float16 or bfloat16 -- go to the ``flash_hypercons::_matrix_exp`` operator,
+whose backward is ``flash_hypercons::_frechet``; both run the HIP kernels of
+``libflash_hypercons_hip.so``.  Everything else uses native PyTorch, as in the
+reference.  Importing this module fails if the compiled extension is missing:
+there is no Python or CPU stand-in for the kernels.
+"""
+
+import functools
+
+import torch
+from torch.overrides import TorchFunctionMode, has_torch_function
+
+from flash_hypercons import _C  # noqa: F401  (registers the flash_hypercons::* operators)
+
+_NATIVE = torch.ops.aten.linalg_matrix_exp.default
+_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+_FUNCTIONS = (torch.linalg.matrix_exp, torch.matrix_exp, torch.Tensor.matrix_exp)
+_ARCH = "gfx950"  # the only code object the extension carries
+
+
+@functools.lru_cache(maxsize=None)
+def _device_supported(index: int) -> bool:
+    return torch.cuda.get_device_properties(index).gcnArchName.split(":")[0] == _ARCH
+
+
+def _eligible(input: torch.Tensor) -> bool:
+    """Reference ops/matrix_exp/__init__.py:13-23, with the platform test flipped to ROCm/gfx950."""
+    return (
+        isinstance(input, torch.Tensor)
+        and input.device.type == "cuda"
+        and torch.version.hip is not None
+        and input.layout == torch.strided
+        and input.ndim == 3
+        and input.shape[-1] == input.shape[-2]
+        and 1 < input.shape[-1] <= 32
+        and input.dtype in _DTYPES
+        and _device_supported(input.device.index)
+    )
+
+
+def _native(input: torch.Tensor, *, promote: bool = False) -> torch.Tensor:
+    """Reference :26-29: native exponential, FP32-promoted for GPU low precision when asked."""
+    if promote and input.is_cuda and input.dtype in (torch.float16, torch.bfloat16):
+        return _NATIVE(input.float()).to(input.dtype)
+    return _NATIVE(input)
+
+
+def _frechet_reference(input: torch.Tensor, direction: torch.Tensor) -> torch.Tensor:
+    """Reference :32-37: differentiable Frechet derivative via the 2N x 2N block exponential."""
+    n = input.shape[-1]
+    a, g = input.float(), direction.float()
+    zero = torch.zeros_like(a)
+    block = torch.cat((torch.cat((a, g), -1), torch.cat((zero, a), -1)), -2)
+    return _NATIVE(block)[..., :n, n:].to(input.dtype)
+
+
+@torch.library.register_fake("flash_hypercons::_matrix_exp")
+def _matrix_exp_fake(input):
+    """Reference :40-49."""
+    torch._check(input.device.type == "cuda")
+    torch._check(input.layout == torch.strided)
+    torch._check(input.ndim == 3)
+    torch._check(input.dtype in _DTYPES)
+    torch._check(input.shape[-1] == input.shape[-2])
+    torch._check(input.shape[-1] > 1)
+    torch._check(input.shape[-1] <= 32)
+    return input.new_empty(input.shape)
+
+
+@torch.library.register_fake("flash_hypercons::_frechet")
+def _frechet_fake(input, direction):
+    """Reference :52-58."""
+    torch._check(direction.shape == input.shape)
+    torch._check(direction.device == input.device)
+    torch._check(direction.dtype == input.dtype)
+    torch._check(direction.layout == torch.strided)
+    return _matrix_exp_fake(input)
+
+
+@torch.library.register_fake("flash_hypercons::_expm_params")
+def _expm_params_fake(input, direction=None):
+    _matrix_exp_fake(input)
+    return input.new_empty((input.shape[0], 2), dtype=torch.int32), input.new_empty((input.shape[0],), dtype=torch.float64)
+
+
+@torch.library.register_fake("flash_hypercons::_expm_debug")
+def _expm_debug_fake(input, direction, variant):
+    return _matrix_exp_fake(input), input.new_empty((input.shape[0],), dtype=torch.int32)
+
+
+def _setup_context(ctx, inputs, output):
+    ctx.save_for_backward(inputs[0])
+
+
+def _backward(ctx, grad_output):
+    """Reference :65-74: the gradient of exp at A against G is L(A^T, G)."""
+    (input,) = ctx.saved_tensors
+    if (
+        torch.is_grad_enabled()
+        or has_torch_function((input, grad_output))
+        or torch.autograd.forward_ad.unpack_dual(input).tangent is not None
+        or torch.autograd.forward_ad.unpack_dual(grad_output).tangent is not None
+    ):
+        return _frechet_reference(input.mT, grad_output)
+    return torch.ops.flash_hypercons._frechet(input.mT, grad_output)
+
+
+torch.library.register_autograd("flash_hypercons::_matrix_exp", _backward, setup_context=_setup_context)
+
+
+def matrix_exp(input: torch.Tensor) -> torch.Tensor:
+    """Compute exp(input), accelerating ROCm [B, N, N] tensors with 2 <= N <= 32 on gfx950.
+
+    The HIP implementation accepts float32, float16, and bfloat16. Other
+    inputs use native PyTorch. Forward AD, function transforms, and tensor
+    subclasses also use native operations; their GPU low-precision inputs
+    are promoted to float32 for the calculation and cast back on return.
+    """
+    # Check transforms before shape eligibility: vmap can hide batch dimensions.
+    if isinstance(input, torch.Tensor) and (
+        type(input) not in (torch.Tensor, torch.nn.Parameter)
+        or torch._C._are_functorch_transforms_active()
+        or torch.autograd.forward_ad.unpack_dual(input).tangent is not None
+    ):
+        return _native(input, promote=True)
+    if not _eligible(input):
+        return _native(input)
+    return torch.ops.flash_hypercons._matrix_exp(input)
+
+
+class _MatrixExpMode(TorchFunctionMode):
+    """Reference :100-108: reroutes the three matrix-exp entry points, nothing else."""
+
+    def __torch_function__(self, func, types, args=(), kwargs=None):
+        kwargs = kwargs or {}
+        if func in _FUNCTIONS:
+            if len(args) == 1 and not kwargs:
+                return matrix_exp(args[0])
+            if not args and set(kwargs) == {"input"}:
+                return matrix_exp(kwargs["input"])
+        return func(*args, **kwargs)
+
+
+def use_backend() -> TorchFunctionMode:
+    """Route Python matrix-exp calls through flash-hypercons within a with block.
+
+    Scopes nest and restore normal routing on exit, including exceptional exit.
+    Enter the scope around calls to compiled functions as well as eager calls.
+    Direct ATen/C++ calls are unaffected.
+    """
+    return _MatrixExpMode()
+
+
+__all__ = ["matrix_exp", "use_backend"]

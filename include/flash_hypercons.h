@@ -1,0 +1,107 @@
+/*
+ * flash_hypercons.h -- C ABI of the MI355X (gfx950) batched small-matrix
+ * exponential library, libflash_hypercons_hip.so.
+ *
+ * The library computes, for a batch of [B, n, n] matrices with 2 <= n <= 32
+ * stored as float32, float16 or bfloat16:
+ *   forward   exp(X)                                   (degree-18 Taylor,
+ *             Bader-Blanes-Casas 2019, with scaling and squaring)
+ *   Frechet   U block of exp([[X, G], [0, X]])           (the structured
+ *             derivative L(X, G); the autograd backward of exp(A) is
+ *             L(A^T, grad_output))
+ * Arithmetic is FP32 with an FP64 1-norm for the squaring count, as in the
+ * reference.  Inputs are read through arbitrary element strides (transposed,
+ * expanded stride-0 and lazily negated views need no copy); the output is a
+ * contiguous [B, n, n] array in the input dtype.
+ *
+ * All pointers are device pointers of one HIP device, the current device of
+ * the calling thread.  Launches are asynchronous on `stream`; nothing here
+ * synchronises, allocates device memory or keeps state across calls other
+ * than the thread-local error message.
+ *
+ * Return value of every entry point: FH_OK, or an FH_ERR_* code with a
+ * message available from fh_last_error() on the same thread.
+ */
+#ifndef FLASH_HYPERCONS_H
+#define FLASH_HYPERCONS_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#if defined(__GNUC__)
+#define FH_API __attribute__((visibility("default")))
+#else
+#define FH_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FH_OK 0
+#define FH_ERR_INVALID_ARGUMENT 1 /* shape, dtype, pointer or stride not accepted */
+#define FH_ERR_LAUNCH 2           /* a HIP launch reported an error */
+
+/* Element types; the codes are the reference launcher's
+ * (csrc/matrix_exp.cu:17: 0 = float32, 1 = bfloat16, 2 = float16). */
+#define FH_DTYPE_F32 0
+#define FH_DTYPE_BF16 1
+#define FH_DTYPE_F16 2
+
+/* Kernel selection for fh_expm_launch. */
+#define FH_VARIANT_AUTO 0    /* the tuned gfx950 kernels (what fh_matrix_exp/fh_frechet run) */
+#define FH_VARIANT_GENERIC 1 /* one wavefront per matrix in the reference's exact
+                                evaluation order; a checking aid, not a fast path */
+
+/* exp(X) for X = input viewed as [batch, n, n] with element strides
+ * strides[0..2] (batch, row, column) and a lazy-negation flag.
+ * Replaces matrix_exp_cuda (csrc/matrix_exp.cu:80-82), the CUDA kernel of the
+ * schema flash_hypercons::_matrix_exp(Tensor input) -> Tensor
+ * (csrc/register.cpp:11, :16).  Rejects n outside [2, 32] and unknown dtypes
+ * with the reference's message (csrc/matrix_exp.cu:52-55).  batch == 0 is a
+ * no-op (csrc/matrix_exp.cu:62-64). */
+FH_API int fh_matrix_exp(const void* input, const int64_t strides[3], int input_neg, void* out, int dtype,
+                  int64_t batch, int n, hipStream_t stream);
+
+/* U block of exp([[X, G], [0, X]]) with X = input and G = direction, both
+ * [batch, n, n] of the same dtype, each with its own strides and negation flag.
+ * Replaces frechet_cuda (csrc/matrix_exp.cu:84-86), the CUDA kernel of
+ * flash_hypercons::_frechet(Tensor input, Tensor direction) -> Tensor
+ * (csrc/register.cpp:12, :17). */
+FH_API int fh_frechet(const void* input, const int64_t input_strides[3], int input_neg, const void* direction,
+               const int64_t direction_strides[3], int direction_neg, void* out, int dtype, int64_t batch,
+               int n, hipStream_t stream);
+
+/* The launcher under both entry points: direction == NULL selects exp(X),
+ * otherwise the Frechet block.  `variant` picks the kernel family
+ * (FH_VARIANT_*).  When s_out is not NULL it also receives the squaring count
+ * of every matrix (int32 [batch]; -1 where the non-finite rule fired).
+ * Replaces small_matrix_exp_cuda + launch_small_matrix_exp
+ * (csrc/matrix_exp.cu:51-78, :13-33). */
+FH_API int fh_expm_launch(const void* input, const int64_t input_strides[3], int input_neg, const void* direction,
+                   const int64_t direction_strides[3], int direction_neg, void* out, int dtype, int64_t batch,
+                   int n, int variant, int32_t* s_out, hipStream_t stream);
+
+/* Selection parameters only: params (int32 [batch, 2]) receives (degree, s)
+ * per matrix -- degree 18 and the squaring count, or (-1, -1) for a matrix the
+ * non-finite rule sends to NaN -- and norms (double [batch], may be NULL) the
+ * FP64 1-norm the count was derived from (NaN for non-finite matrices).
+ * direction may be NULL (forward) or the Frechet direction (backward norm of
+ * the augmented matrix).  No counterpart in the reference: it exposes the
+ * per-matrix choice made inside MatrixExpSmall.cuh:141-154 / :332-361 so that
+ * it can be checked bit for bit. */
+FH_API int fh_expm_params(const void* input, const int64_t input_strides[3], int input_neg, const void* direction,
+                   const int64_t direction_strides[3], int direction_neg, int dtype, int64_t batch, int n,
+                   int32_t* params, double* norms, hipStream_t stream);
+
+/* Message of the last failing call on this thread ("" if none). */
+FH_API const char* fh_last_error(void);
+
+/* Library version string, e.g. "0.1.0". */
+FH_API const char* fh_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASH_HYPERCONS_H */

@@ -1,0 +1,95 @@
+"""FP64 checks used by the tests.
+
+``reference`` and ``check_error`` restate the reference repository's own test
+oracle (tests/reference.py:4-22 there): native FP64 ``linalg_matrix_exp`` of the
+matrix, or of the block matrix [[A, G], [0, A]] for the Frechet derivative, and
+the per-matrix error max|actual - ref| / (1 + max|ref|) with tolerances 1e-3 /
+5e-3 (FP32 forward / backward) and 0.05 / 0.1 (FP16, BF16).
+
+``check_north_star`` applies the tighter contract this build is held to:
+FP32 relative Frobenius error <= 1e-5 forward and <= 1e-4 backward per matrix;
+FP16/BF16 every element within one output-dtype ulp of the FP64 reference
+rounded to that dtype (absolute floor: one ulp of the matrix's largest |ref|),
+with infinities matching the rounded reference exactly.
+"""
+
+import torch
+
+FWD_REL_FRO = 1e-5
+BWD_REL_FRO = 1e-4
+
+
+def reference(a, direction=None):
+    a = a.double()
+    if direction is None:
+        return torch.ops.aten.linalg_matrix_exp.default(a)
+    n = a.shape[-1]
+    zero = torch.zeros_like(a)
+    block = torch.cat((torch.cat((a, direction.double()), -1), torch.cat((zero, a), -1)), -2)
+    return torch.ops.aten.linalg_matrix_exp.default(block)[..., :n, n:]
+
+
+def check_error(actual, expected, *, backward=False):
+    assert actual.shape == expected.shape
+    if not actual.numel():
+        return
+    assert actual.isfinite().all()
+    tolerance = (0.005 if backward else 0.001) if actual.dtype == torch.float32 else (0.1 if backward else 0.05)
+    delta = (actual.double() - expected.double().to(actual.device)).abs().flatten(-2).amax(-1)
+    scale = 1 + expected.double().to(actual.device).abs().flatten(-2).amax(-1)
+    torch.testing.assert_close(delta / scale, torch.zeros_like(delta), atol=tolerance, rtol=0)
+
+
+def _mant(dtype):
+    return {torch.float16: 10, torch.bfloat16: 7, torch.float32: 23}[dtype]
+
+
+def ulp(x, dtype):
+    finfo = torch.finfo(dtype)
+    ax = x.abs().clamp_min(finfo.tiny)
+    return torch.pow(2.0, torch.floor(torch.log2(ax)) - _mant(dtype))
+
+
+def rel_frobenius(actual, ref64):
+    ref64 = ref64.to(actual.device)
+    num = (actual.double() - ref64).flatten(-2).norm(dim=-1)
+    den = ref64.flatten(-2).norm(dim=-1).clamp_min(1e-300)
+    return num / den
+
+
+def check_north_star(actual, ref64, *, backward=False):
+    """Per-matrix contract; returns the worst error measure for reporting."""
+    assert actual.shape == ref64.shape
+    if not actual.numel():
+        return 0.0
+    ref64 = ref64.to(actual.device)
+    if actual.dtype == torch.float32:
+        err = rel_frobenius(actual, ref64)
+        bound = BWD_REL_FRO if backward else FWD_REL_FRO
+        worst = err.max().item()
+        assert worst <= bound, f"relative Frobenius error {worst:.3e} > {bound:.0e}"
+        return worst
+    rounded = ref64.to(actual.dtype)
+    inf_ref = rounded.isinf()
+    assert torch.equal(actual.isinf(), inf_ref), "infinity pattern differs from the rounded FP64 reference"
+    assert torch.equal(actual[inf_ref], rounded[inf_ref]), "infinity signs differ"
+    assert not actual.isnan().any()
+    # Faithful rounding: the output is one of the two dtype values that
+    # bracket the FP64 reference, i.e. |actual - ref| <= one ulp taken at the
+    # larger of |actual|, |ref| (one ulp of the matrix's largest |ref| for
+    # tiny, cancelling entries).
+    fin = ~inf_ref
+    act = torch.where(fin, actual.double(), torch.zeros_like(ref64))
+    finite_ref = torch.where(fin, ref64, torch.zeros_like(ref64))
+    diff = (act - finite_ref).abs()
+    floor = ulp(finite_ref.abs().flatten(-2).amax(-1), actual.dtype)[..., None, None]
+    tol = torch.maximum(ulp(torch.maximum(act.abs(), finite_ref.abs()), actual.dtype), floor)
+    excess = diff / tol
+    worst = excess.max().item()
+    if worst > 1.0:
+        idx = tuple(int(i) for i in torch.nonzero(excess == excess.max())[0])
+        raise AssertionError(
+            f"element {idx} off by {worst:.4f} output ulps: actual {act[idx].item()!r} "
+            f"reference {finite_ref[idx].item()!r} ({actual.dtype})"
+        )
+    return worst

@@ -1,0 +1,317 @@
+"""Throughput of the batched small-matrix exponential (forward + Frechet backward) on one MI355X.
+
+Headline (``value``): BASELINE config 2 -- [1048576, 4, 4] FP32, entries N(0, 0.25^2),
+upstream gradient N(0, 1); one step = ``fh.matrix_exp`` forward plus
+``torch.autograd.grad`` backward over the whole batch, inputs resident in HBM.
+Metric: matrices per second of forward + backward.
+
+Also reported in the same JSON line:
+* ``roofline`` -- the dominant kernel of that step (the P = 4 Frechet kernel),
+  algorithmic bytes per launch / its mean launch time from HIP events on the
+  stream it runs on, against MI355X's 8 TB/s;
+* ``cpu_baseline`` -- the CPU restatement (oracle/, scalar C, one thread) over
+  the same workload; ``cpu_native_torch`` -- native torch.linalg.matrix_exp +
+  autograd on the host cores (the reference's own CPU path), on a sample;
+* ``configs`` -- configs 3-5 (BF16 N=4 sweep, strided FP32 N=16, FP16 N=32 and
+  the same shape in FP32) with their own rooflines (HBM for N=4, FP32 MFMA for
+  N>=16, where the flop count uses each matrix's own squaring count).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--only c2]
+"""
+
+from __future__ import annotations
+
+import argparse
+import hashlib
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT / "flash-hyperconnections_amd"), str(ROOT)):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+MFMA_F32_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix
+METRIC = "matrices/sec fwd+bwd (N=4 B=2^20, N=32 B=32768); % HBM/MFMA roofline"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def make_inputs(name: str, torch, device):
+    """Seeded synthetic inputs per BASELINE configs 2-5 (seed 0; base, then per-matrix scale, then grad)."""
+    torch.manual_seed(0)
+    if name == "c2":
+        b, n = 1 << 20, 4
+        x = torch.randn(b, n, n) * 0.25
+        g = torch.randn(b, n, n)
+        dtype, layout = torch.float32, "contiguous"
+    elif name == "c3":
+        b, n = 1 << 20, 4
+        base = torch.randn(b, n, n)
+        base = base / torch.linalg.matrix_norm(base, ord=1)[:, None, None]
+        x = base * (10 ** torch.empty(b).uniform_(-3, 2))[:, None, None]
+        g = torch.randn(b, n, n)
+        dtype, layout = torch.bfloat16, "contiguous"
+    elif name == "c4":
+        b, n = 65536, 16
+        base = torch.randn(b, n, n) / 4 * (10 ** torch.empty(b).uniform_(-1, 1))[:, None, None]
+        x = base
+        g = torch.randn(b, n, n)
+        dtype, layout = torch.float32, "transposed view"
+    elif name in ("c5", "c5f32"):
+        b, n = 32768, 32
+        x = torch.randn(b, n, n) / n**0.5 * (10 ** torch.empty(b).uniform_(-1, 1.5))[:, None, None]
+        g = torch.randn(b, n, n)
+        dtype, layout = (torch.float16 if name == "c5" else torch.float32), "contiguous"
+    else:
+        raise ValueError(name)
+    x = x.to(dtype).to(device)
+    g = g.to(dtype).to(device)
+    if layout == "transposed view":
+        x = x.transpose(-1, -2)  # noncontiguous input, as BASELINE config 4 specifies
+    return x, g, layout
+
+
+def sha256(t) -> str:
+    import torch
+
+    return hashlib.sha256(t.detach().contiguous().cpu().view(torch.uint8).numpy().tobytes()).hexdigest()
+
+
+def time_loop(torch, fn, iters: int, warmup: int) -> float:
+    """Mean ms per call of fn(), HIP events on the current stream (where the kernels launch)."""
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(iters):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def measure_config(name: str, torch, fh, steps: int, warmup: int, device) -> dict:
+    x, g, layout = make_inputs(name, torch, device)
+    b, n = x.shape[0], x.shape[-1]
+    e = x.element_size()
+    xin = x.detach().requires_grad_()
+
+    def step():
+        y = fh.matrix_exp(xin)
+        return torch.autograd.grad(y, xin, g)[0]
+
+    fwd = torch.ops.flash_hypercons._matrix_exp
+    bwd = torch.ops.flash_hypercons._frechet
+    xt = x.detach().mT
+    ms_step = time_loop(torch, step, steps, warmup)
+    ms_fwd = time_loop(torch, lambda: fwd(x), steps, warmup)
+    ms_bwd = time_loop(torch, lambda: bwd(xt, g), steps, warmup)
+
+    # Graph-captured step (launch overhead removed): same kernels, replayed.
+    ms_graph = None
+    try:
+        gstream = torch.cuda.Stream()
+        gstream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(gstream):
+            for _ in range(3):
+                step()
+        torch.cuda.current_stream().wait_stream(gstream)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        ms_graph = time_loop(torch, graph.replay, steps, 2)
+    except Exception as exc:  # pragma: no cover - reported, not fatal
+        log(f"[bench] graph capture of {name} failed: {exc}")
+
+    params_f, _ = torch.ops.flash_hypercons._expm_params(x)
+    params_b, _ = torch.ops.flash_hypercons._expm_params(xt, g)
+    s_f = params_f[:, 1].clamp_min(0).double()
+    s_b = params_b[:, 1].clamp_min(0).double()
+    bytes_fwd = b * n * n * 2 * e
+    bytes_bwd = b * n * n * 3 * e
+    flops_fwd = float(((5 + s_f) * 2 * n**3).sum())
+    flops_bwd = float(((5 + s_b) * 3 * 2 * n**3).sum())
+    t_hbm = (bytes_fwd + bytes_bwd) / (HBM_PEAK_GBS * 1e9)
+    t_mfma = (flops_fwd + flops_bwd) / (MFMA_F32_PEAK_TFLOPS * 1e12)
+    bound = "hbm" if n <= 8 else "mfma"
+    t_ideal = t_hbm if bound == "hbm" else t_mfma
+    out = {
+        "shape": [b, n, n],
+        "dtype": str(x.dtype).replace("torch.", ""),
+        "layout": layout,
+        "matrices_per_s_fwd_bwd": b / (ms_step * 1e-3),
+        "ms_step": ms_step,
+        "ms_step_graph": ms_graph,
+        "ms_fwd_kernel": ms_fwd,
+        "ms_bwd_kernel": ms_bwd,
+        "mean_s_fwd": float(s_f.mean()),
+        "mean_s_bwd": float(s_b.mean()),
+        "bound": bound,
+        "roofline_frac_step": t_ideal / (ms_step * 1e-3),
+        "fwd_kernel": {
+            "achieved_gbs": bytes_fwd / (ms_fwd * 1e-3) / 1e9,
+            "achieved_tflops": flops_fwd / (ms_fwd * 1e-3) / 1e12,
+        },
+        "bwd_kernel": {
+            "achieved_gbs": bytes_bwd / (ms_bwd * 1e-3) / 1e9,
+            "achieved_tflops": flops_bwd / (ms_bwd * 1e-3) / 1e12,
+        },
+        "input_sha256": sha256(x)[:16],
+        "grad_sha256": sha256(g)[:16],
+    }
+    if bound == "hbm":
+        out["fwd_kernel"]["frac"] = out["fwd_kernel"]["achieved_gbs"] / HBM_PEAK_GBS
+        out["bwd_kernel"]["frac"] = out["bwd_kernel"]["achieved_gbs"] / HBM_PEAK_GBS
+    else:
+        out["fwd_kernel"]["frac"] = out["fwd_kernel"]["achieved_tflops"] / MFMA_F32_PEAK_TFLOPS
+        out["bwd_kernel"]["frac"] = out["bwd_kernel"]["achieved_tflops"] / MFMA_F32_PEAK_TFLOPS
+    del xin, x, g, xt
+    return out
+
+
+def cpu_oracle_baseline(torch) -> dict:
+    """The CPU restatement (scalar C, 1 thread) over the full config-2 workload."""
+    import numpy as np
+
+    import oracle
+
+    x, g, _ = make_inputs("c2", torch, "cpu")
+    xf = oracle.tensor_to_f32(x)
+    gf = oracle.tensor_to_f32(g)
+    xt = np.ascontiguousarray(xf.transpose(0, 2, 1))
+    t0 = time.perf_counter()
+    oracle.matrix_exp_f32(xf)
+    oracle.matrix_exp_f32(xt, gf)
+    dt = time.perf_counter() - t0
+    return {
+        "value": x.shape[0] / dt,
+        "unit": "matrices/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"all {x.shape[0]} config-2 matrices, forward + Frechet backward, oracle/fh_oracle.c "
+        f"(scalar C restatement, one thread), {dt:.2f} s",
+    }
+
+
+def cpu_native_torch(torch, sample: int = 1 << 18) -> dict:
+    """Native torch.linalg.matrix_exp + autograd on host cores (the reference's CPU path)."""
+    x, g, _ = make_inputs("c2", torch, "cpu")
+    x = x[:sample].clone().requires_grad_()
+    g = g[:sample].clone()
+    threads = torch.get_num_threads()
+    y = torch.linalg.matrix_exp(x[:1024])  # warm
+    torch.autograd.grad(y.sum(), x)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        y = torch.linalg.matrix_exp(x)
+        torch.autograd.grad(y, x, g)
+        times.append(time.perf_counter() - t0)
+    dt = statistics.median(times)
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": sample / dt,
+        "unit": "matrices/s",
+        "cores": threads,
+        "cpu_count": os.cpu_count(),
+        "cpu_model": model,
+        "sample": f"first {sample} config-2 matrices, torch.linalg.matrix_exp + autograd.grad, median of 3",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baselines")
+    ap.add_argument("--only", default=None, help="comma list of configs (c2,c3,c4,c5,c5f32)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one GPU: the operator has no cross-GPU step (every matrix is independent; "
+            f"B shards contiguously with no exchange), and this build runs on single-GPU boxes. "
+            f"--gpus {args.gpus} is not supported.",
+            file=sys.stderr,
+        )
+        return 2
+    import torch
+
+    import flash_hypercons as fh
+
+    device = torch.device("cuda:0")
+    configs = (args.only or "c2,c3,c4,c5,c5f32").split(",")
+    results = {}
+    for name in configs:
+        log(f"[bench] {name} ...")
+        results[name] = measure_config(name, torch, fh, args.steps, args.warmup, device)
+        log(f"[bench] {name}: {json.dumps(results[name])}")
+        torch.cuda.empty_cache()
+
+    head = results.get("c2")
+    line = {
+        "metric": METRIC,
+        "value": head["matrices_per_s_fwd_bwd"] if head else None,
+        "unit": "matrices/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_step"] if head else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded, BASELINE config 2 distribution)",
+        "config": {
+            "workload": "BASELINE config 2: fh.matrix_exp forward + autograd backward on [1048576,4,4] FP32, "
+            "x ~ N(0,0.25^2), grad ~ N(0,1)",
+            "global_batch": 1 << 20,
+            "n": 4,
+            "parallelism": "single GPU",
+        },
+    }
+    if head:
+        b = 1 << 20
+        bytes_bwd = b * 16 * 3 * 4
+        achieved = head["bwd_kernel"]["achieved_gbs"]
+        line["roofline"] = {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None,
+            "kernel": "expm_quad_kernel<F32, Pair=true> (Frechet backward, P=4)",
+            "algorithmic_bytes_per_launch": bytes_bwd,
+            "mean_launch_ms": head["ms_bwd_kernel"],
+        }
+        line["step_roofline_frac"] = head["roofline_frac_step"]
+    if not args.skip_cpu:
+        log("[bench] cpu baselines ...")
+        line["cpu_baseline"] = cpu_oracle_baseline(torch)
+        line["cpu_native_torch"] = cpu_native_torch(torch)
+    line["configs"] = results
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -33,7 +33,7 @@ HIPCC = str(ROCM / "bin" / "hipcc")
 LIB_NAME = "libflash_hypercons_hip.so"
 KERNEL_SOURCES = [
     "expm_generic.hip",
-    "expm_quad.hip",
+    "expm_p4.hip",
     "expm_oct.hip",
     "expm_tile.hip",
     "expm_params.hip",
@@ -41,7 +41,8 @@ KERNEL_SOURCES = [
 ]
 
 # -ffp-contract=off: every fused multiply-add in the kernels is written out.
-# The packed-FP32 feature is switched off (v_pk_*_f32 stay out of the code).
+# The packed-FP32 feature is switched off (no packed FP32 instructions are
+# generated).
 HIP_FLAGS = [
     "-x", "hip",
     "-O3",
@@ -51,6 +52,9 @@ HIP_FLAGS = [
     "-ffp-contract=off",
     "-fno-gpu-flush-denormals-to-zero",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results stay in ordinary VGPRs (no accumulator-register copies
+    # between chained products).
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-fvisibility=hidden",
     "-Wall",
     f"-I{INCLUDE}",

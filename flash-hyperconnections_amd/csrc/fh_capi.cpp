@@ -86,7 +86,7 @@ int launch(const void* input, const int64_t input_strides[3], int input_neg, con
   if (variant == FH_VARIANT_GENERIC) {
     err = fh::launch_generic(args, dtype, P, pair, stream);
   } else if (P == 4) {
-    err = fh::launch_quad(args, dtype, pair, stream);
+    err = fh::launch_p4(args, dtype, pair, stream);
   } else if (P == 8) {
     err = fh::launch_oct(args, dtype, pair, stream);
   } else {
@@ -98,6 +98,21 @@ int launch(const void* input, const int64_t input_strides[3], int input_neg, con
 }
 
 }  // namespace
+
+namespace fh {
+
+int64_t resident_blocks(const void* kernel, int block) {
+  int device = 0;
+  int per_cu = 0;
+  int cus = 0;
+  if (hipGetDevice(&device) != hipSuccess) return 1;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, 0) != hipSuccess) per_cu = 1;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) cus = 1;
+  const int64_t n = static_cast<int64_t>(per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+  return n > 0 ? n : 1;
+}
+
+}  // namespace fh
 
 extern "C" {
 

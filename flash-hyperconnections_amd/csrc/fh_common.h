@@ -46,9 +46,9 @@ struct F16 {
 
 // One [batch, n, n] operand read through element strides.  `sign` is -1 for
 // a lazily negated tensor view and +1 otherwise (multiplying by it is exact).
-// `vec` tells the P == 4 kernel that whole rows (kVecRows: sc == 1) or whole
-// columns (kVecCols: sr == 1) of a 4 x 4 matrix are contiguous and aligned for
-// one vector load; the host sets it only when n == 4 and alignment holds.
+// `vec` tells the P == 4 kernel that every row (kVecRows: sc == 1) or every
+// column (kVecCols: sr == 1) of a 4 x 4 matrix is one aligned 4-element
+// vector; the host sets it only when n == 4 and the alignment holds.
 constexpr int kVecNone = 0;
 constexpr int kVecRows = 1;
 constexpr int kVecCols = 2;
@@ -107,6 +107,10 @@ __device__ __forceinline__ void store_elem(void* out, int64_t idx, float v) {
   static_cast<typename T::storage*>(out)[idx] = from_f32<T>(v);
 }
 
+// ceil(log2(q)) through the library log2; kept out of line because only the
+// rare band below needs it.
+static __device__ __attribute__((noinline)) int ceil_log2_library(double q) { return static_cast<int>(ceil(log2(q))); }
+
 // s = norm > theta18 ? ceil(log2(norm / theta18)) : 0, in double (reference
 // csrc/MatrixExpSmall.cuh:154, :356).  For q = norm/theta18 = m * 2^e with
 // m in [0.5, 1): ceil(log2 q) is e - 1 when m == 0.5 and e otherwise, and any
@@ -118,7 +122,7 @@ __device__ __forceinline__ int squarings_from_norm(double norm) {
   int e;
   const double m = frexp(q, &e);
   if (m == 0.5) return e - 1;
-  if (m < 0.5 + 0x1p-41) return static_cast<int>(ceil(log2(q)));
+  if (m < 0.5 + 0x1p-41) return ceil_log2_library(q);
   return e;
 }
 

@@ -4,8 +4,8 @@
   oracle for every matrix, in both directions, for every size class and dtype.
 * The generic kernel (FH_VARIANT_GENERIC) evaluates in the reference's exact
   order and must match the oracle bit for bit.
-* The tuned P == 4 kernel keeps the reference's order on 4x4x1 MFMA steps and
-  must also match the oracle bit for bit.
+* The tuned P == 4 kernel (one matrix per lane, plain FP32 FMAs) keeps the
+  reference's evaluation order and must also match the oracle bit for bit.
 * Every kernel must meet the FP32 / FP16 / BF16 tolerances against FP64.
 Inputs are seeded; GPU results are compared through the C ABI that the
 ``flash_hypercons::_expm_debug`` / ``_expm_params`` operators wrap.
@@ -122,3 +122,37 @@ def test_nonfinite_rule_matches_oracle(n):
             ok, bad = same_values(out, exp_out) if variant == GENERIC else (True, 0)
             assert ok, f"{bad} elements differ"
             assert torch.equal(out.isnan().cpu(), exp_out.isnan())
+
+
+def test_config1_golden_fixture_on_gpu():
+    """BASELINE config 1 inputs on the GPU path against the committed FP64 fixture."""
+    from pathlib import Path
+
+    import numpy as np
+
+    import flash_hypercons as fh
+    from tests.reference import rel_frobenius
+
+    d = np.load(Path(__file__).resolve().parent / "golden" / "c1_cpu_plumbing.npz")
+    x = torch.from_numpy(d["x"]).cuda().requires_grad_()
+    y = fh.matrix_exp(x)
+    (grad,) = torch.autograd.grad(y.sum(), x)
+    assert rel_frobenius(y.detach().cpu(), torch.from_numpy(d["y"])).max() <= 1e-5
+    assert rel_frobenius(grad.cpu(), torch.from_numpy(d["grad"])).max() <= 1e-4
+    exp_out, _ = oracle.torch_matrix_exp(x.detach().cpu())
+    ok, bad = same_values(y.detach(), exp_out)
+    assert ok, f"{bad} elements differ from the oracle"
+
+
+@pytest.mark.parametrize("n", [4, 8, 16, 32])
+def test_squaring_boundary_fixture_on_gpu(n):
+    from pathlib import Path
+
+    import numpy as np
+
+    d = np.load(Path(__file__).resolve().parent / "golden" / "s_boundaries.npz")
+    x = torch.from_numpy(d[f"x{n}"]).cuda()
+    params, _ = torch.ops.flash_hypercons._expm_params(x)
+    assert params[:, 1].cpu().tolist() == d[f"s{n}"].tolist()
+    _, s = run_kernel(x, None, AUTO)
+    assert s.cpu().tolist() == d[f"s{n}"].tolist()

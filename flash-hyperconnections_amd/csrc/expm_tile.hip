@@ -11,8 +11,15 @@
 // steps together cover k = 0..P-1 and
 //   X.Y = sum_r mfma(a = (X^T).v[r], b = Y.v[r])
 // needs no data movement for Y.  Left operands are transposed through a
-// padded LDS tile (P x (P+1) floats).  The kernel is MFMA-bound, so the
-// polynomial's combines stay on the otherwise idle VALU.
+// padded LDS tile (P x (P+1) floats).
+//
+// The MFMA pipe and the VALU do not execute concurrently on gfx950, so every
+// VALU instruction adds to the MFMA time; the kernel keeps VALU work to the
+// combines, one transpose per left operand and the loads/stores.  It is
+// persistent: each wavefront walks matrices with a grid stride and issues the
+// next matrix's loads before computing the current one.  The evaluation
+// order keeps at most four powers and three temporaries live so that two
+// wavefronts fit per SIMD at P = 32.
 #include "fh_kernels.h"
 
 namespace fh {
@@ -117,32 +124,66 @@ __device__ __forceinline__ PTm<P, Pair> ptranspose(const PTm<P, Pair>& a, float*
   return c;
 }
 
-// B(k+1) = c0*I + c1*A + c2*A^2 + c3*A^3 + c6*A^6 as the reference's
-// contracted chain (csrc/MatrixExpSmall.cuh:268-281); identity on D only.
-template <int P, bool Pair>
+// B(K+1) = c0*I + c1*A + c2*A^2 + c3*A^3 + c6*A^6 (csrc/MatrixExpSmall.cuh:
+// 268-281) with zero coefficients skipped; identity on D only.
+template <int K, int P, bool Pair>
 __device__ __forceinline__ PTm<P, Pair> combine(const PTm<P, Pair>& a, const PTm<P, Pair>& a2,
-                                                const PTm<P, Pair>& a3, const PTm<P, Pair>& a6, int k,
+                                                const PTm<P, Pair>& a3, const PTm<P, Pair>& a6,
                                                 const float (&diag)[TileCfg<P>::R]) {
+  constexpr float c0 = kCoef[K][0], c1 = kCoef[K][1], c2 = kCoef[K][2], c3 = kCoef[K][3], c6 = kCoef[K][4];
   PTm<P, Pair> b;
 #pragma unroll
   for (int r = 0; r < TileCfg<P>::R; ++r) {
-    float t = kCoef[k][0] * diag[r];
-    t = __builtin_fmaf(kCoef[k][1], a.d.v[r], t);
-    t = __builtin_fmaf(kCoef[k][2], a2.d.v[r], t);
-    t = __builtin_fmaf(kCoef[k][3], a3.d.v[r], t);
-    b.d.v[r] = __builtin_fmaf(kCoef[k][4], a6.d.v[r], t);
+    float t;
+    if constexpr (c1 != 0.f) {
+      t = __builtin_fmaf(c1, a.d.v[r], c0 * diag[r]);
+    } else {
+      t = c0 * diag[r];
+    }
+    t = __builtin_fmaf(c2, a2.d.v[r], t);
+    t = __builtin_fmaf(c3, a3.d.v[r], t);
+    if constexpr (c6 != 0.f) t = __builtin_fmaf(c6, a6.d.v[r], t);
+    b.d.v[r] = t;
     if constexpr (Pair) {
-      float w = kCoef[k][1] * a.u.v[r];
-      w = __builtin_fmaf(kCoef[k][2], a2.u.v[r], w);
-      w = __builtin_fmaf(kCoef[k][3], a3.u.v[r], w);
-      b.u.v[r] = __builtin_fmaf(kCoef[k][4], a6.u.v[r], w);
+      float w = (c1 != 0.f) ? __builtin_fmaf(c2, a2.u.v[r], c1 * a.u.v[r]) : c2 * a2.u.v[r];
+      w = __builtin_fmaf(c3, a3.u.v[r], w);
+      if constexpr (c6 != 0.f) w = __builtin_fmaf(c6, a6.u.v[r], w);
+      b.u.v[r] = w;
     }
   }
   return b;
 }
 
-template <typename T, int P, bool Pair>
-__global__ __launch_bounds__(64) void expm_tile_kernel(ExpmArgs args) {
+// Layout classes for loading: rows contiguous (sc == 1) loads the D layout of
+// the matrix itself; columns contiguous (sr == 1) loads the D layout of its
+// transpose; anything else gathers element-wise through the strides.
+constexpr int kLoadRows = 0;
+constexpr int kLoadCols = 1;
+
+template <typename T, int P>
+__device__ __forceinline__ Tm<P> load_tile(const Operand& op, int64_t b, int n, int lane, bool transposed) {
+  using C = TileCfg<P>;
+  const int c = C::col(lane);
+  Tm<P> m;
+#pragma unroll
+  for (int r = 0; r < C::R; ++r) {
+    const int row = C::row(lane, r);
+    const bool in = row < n && c < n;
+    // transposed: element (row, c) of M^T, i.e. M[c][row]
+    m.v[r] = in ? load_elem_nosign<T>(op, b, transposed ? c : row, transposed ? row : c) : 0.f;
+  }
+  return m;
+}
+
+// Occupancy target (wavefronts per SIMD) the register allocation must meet.
+template <int P, bool Pair>
+constexpr int kTileWaves() {
+  return P == 16 ? 4 : (Pair ? 1 : 2);
+}
+
+template <typename T, int P, bool Pair, int XL, int GL>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kTileWaves<P, Pair>(), 8))) void expm_tile_kernel(
+    ExpmArgs args) {
   using C = TileCfg<P>;
   constexpr int R = C::R;
   constexpr int LD = P + 1;
@@ -155,34 +196,43 @@ __global__ __launch_bounds__(64) void expm_tile_kernel(ExpmArgs args) {
 #pragma unroll
   for (int r = 0; r < R; ++r) diag[r] = (C::row(lane, r) == c) ? 1.f : 0.f;
 
-  for (int64_t b = blockIdx.x; b < args.batch; b += gridDim.x) {
-    PTm<P, Pair> a, at;
-    bool bad = false;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int row = C::row(lane, r);
-      const bool in = row < n && c < n;
-      a.d.v[r] = in ? load_elem<T>(args.x, b, row, c) : 0.f;
-      at.d.v[r] = in ? load_elem<T>(args.x, b, c, row) : 0.f;
-      bad |= !finite_f32(a.d.v[r]);
-      if constexpr (Pair) {
-        a.u.v[r] = in ? load_elem<T>(args.g, b, row, c) : 0.f;
-        at.u.v[r] = in ? load_elem<T>(args.g, b, c, row) : 0.f;
-        bad |= !finite_f32(a.u.v[r]);
-      }
+  int64_t b = blockIdx.x;
+  Tm<P> nx, ng;
+  if (b < args.batch) {
+    nx = load_tile<T, P>(args.x, b, n, lane, XL == kLoadCols);
+    if constexpr (Pair) ng = load_tile<T, P>(args.g, b, n, lane, GL == kLoadCols);
+  }
+  for (; b < args.batch; b += gridDim.x) {
+    const Tm<P> lx = nx;
+    Tm<P> lg;
+    if constexpr (Pair) lg = ng;
+    if (b + gridDim.x < args.batch) {
+      nx = load_tile<T, P>(args.x, b + gridDim.x, n, lane, XL == kLoadCols);
+      if constexpr (Pair) ng = load_tile<T, P>(args.g, b + gridDim.x, n, lane, GL == kLoadCols);
     }
-    // Non-finite rule (csrc/MatrixExpSmall.cuh:318-331).
-    if (__syncthreads_or(bad)) {
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int row = C::row(lane, r);
-        if (row < n && c < n) store_elem<T>(args.out, (b * n + row) * n + c, __builtin_nanf(""));
+
+    // Both layouts of X (and G) through the LDS tile; the tile that holds the
+    // plain layout also feeds the column sums of the norm.
+    PTm<P, Pair> a, at;
+    if constexpr (XL == kLoadCols) {
+      at.d = lx;
+      a.d = transpose<P>(lx, buf, lane);
+    } else {
+      a.d = lx;
+      at.d = transpose<P>(lx, buf, lane);
+    }
+    if constexpr (Pair) {
+      if constexpr (GL == kLoadCols) {
+        at.u = lg;
+        a.u = transpose<P>(lg, buf, lane);
+      } else {
+        a.u = lg;
+        at.u = transpose<P>(lg, buf, lane);
       }
-      if (lane == 0 && args.s_out) args.s_out[b] = -1;
-      continue;
     }
     // FP64 1-norm, rows summed sequentially per column, |A| then |G| per row
-    // (csrc/MatrixExpSmall.cuh:343-357).
+    // (csrc/MatrixExpSmall.cuh:343-357); the total of the column sums is
+    // finite exactly when every entry is (non-finite rule, :318-331).
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       buf[C::row(lane, r) * LD + c] = a.d.v[r];
@@ -198,33 +248,52 @@ __global__ __launch_bounds__(64) void expm_tile_kernel(ExpmArgs args) {
       colsum[lane] = v;
     }
     __syncthreads();
-    double norm = 0.;
-    for (int j = 0; j < P; ++j) norm = fmax(norm, colsum[j]);
-    const int s = squarings_from_norm(norm);
+    double norm = 0., total = 0.;
+    for (int j = 0; j < P; ++j) {
+      norm = fmax(norm, colsum[j]);
+      total += colsum[j];
+    }
+    const bool bad = !__builtin_isfinite(total);
+    const int s = bad ? 0 : squarings_from_norm(norm);
     __syncthreads();
 
+    if (bad) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int row = C::row(lane, r);
+        if (row < n && c < n) store_elem<T>(args.out, (b * n + row) * n + c, __builtin_nanf(""));
+      }
+      if (lane == 0 && args.s_out) args.s_out[b] = -1;
+      continue;
+    }
+
+    // Scale by 2^-s (csrc/MatrixExpSmall.cuh:362-367), the views' lazy
+    // negation folded into the same exact multiply.
     const float scale = __builtin_ldexpf(1.f, -s);
+    const float scale_x = scale * args.x.sign;
+    const float scale_g = scale * args.g.sign;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      a.d.v[r] *= scale;
-      at.d.v[r] *= scale;
+      a.d.v[r] *= scale_x;
+      at.d.v[r] *= scale_x;
       if constexpr (Pair) {
-        a.u.v[r] *= scale;
-        at.u.v[r] *= scale;
+        a.u.v[r] *= scale_g;
+        at.u.v[r] *= scale_g;
       }
     }
+
     // Degree-18 polynomial.  Powers are formed as A.A and A.A^2 (all factors
-    // are polynomials in the same matrix), then A^6 = A^3.A^3, A9 = B1.B5 + B4,
-    // T = B2 + (B3 + A9).A9.
+    // are polynomials in the same matrix), then A^6 = A^3.A^3,
+    // A9 = B1.B5 + B4 and T = B2 + (B3 + A9).A9.
     const PTm<P, Pair> a2 = pmm<P, Pair>(at, a);
     const PTm<P, Pair> a3 = pmm<P, Pair>(at, a2);
     const PTm<P, Pair> a6 = pmm<P, Pair>(ptranspose<P, Pair>(a3, buf, lane), a3);
-    const PTm<P, Pair> b1t = ptranspose<P, Pair>(combine<P, Pair>(a, a2, a3, a6, 0, diag), buf, lane);
-    const PTm<P, Pair> b5 = combine<P, Pair>(a, a2, a3, a6, 4, diag);
-    const PTm<P, Pair> a9 = padd<P, Pair>(pmm<P, Pair>(b1t, b5), combine<P, Pair>(a, a2, a3, a6, 3, diag));
+    PTm<P, Pair> a9 = pmm<P, Pair>(ptranspose<P, Pair>(combine<0, P, Pair>(a, a2, a3, a6, diag), buf, lane),
+                                   combine<4, P, Pair>(a, a2, a3, a6, diag));
+    a9 = padd<P, Pair>(a9, combine<3, P, Pair>(a, a2, a3, a6, diag));
     const PTm<P, Pair> lhst =
-        ptranspose<P, Pair>(padd<P, Pair>(combine<P, Pair>(a, a2, a3, a6, 2, diag), a9), buf, lane);
-    const PTm<P, Pair> b2 = combine<P, Pair>(a, a2, a3, a6, 1, diag);
+        ptranspose<P, Pair>(padd<P, Pair>(combine<2, P, Pair>(a, a2, a3, a6, diag), a9), buf, lane);
+    const PTm<P, Pair> b2 = combine<1, P, Pair>(a, a2, a3, a6, diag);
     PTm<P, Pair> res = padd<P, Pair>(b2, pmm<P, Pair>(lhst, a9));
     for (int i = 0; i < s; ++i) res = pmm<P, Pair>(ptranspose<P, Pair>(res, buf, lane), res);
 
@@ -237,11 +306,33 @@ __global__ __launch_bounds__(64) void expm_tile_kernel(ExpmArgs args) {
   }
 }
 
+template <typename T, int P, bool Pair, int XL, int GL>
+hipError_t launch_tile_l(const ExpmArgs& args, hipStream_t stream) {
+  static const int64_t resident =
+      resident_blocks(reinterpret_cast<const void*>(&expm_tile_kernel<T, P, Pair, XL, GL>), 64);
+  const int64_t grid = args.batch < resident ? args.batch : resident;
+  hipLaunchKernelGGL((expm_tile_kernel<T, P, Pair, XL, GL>), dim3(static_cast<unsigned>(grid)), dim3(64), 0, stream,
+                     args);
+  return hipGetLastError();
+}
+
+int load_class(const Operand& op) { return (op.sr == 1 && op.sc != 1) ? kLoadCols : kLoadRows; }
+
 template <typename T, int P, bool Pair>
 hipError_t launch_tile_tp(const ExpmArgs& args, hipStream_t stream) {
-  const int64_t grid = args.batch < (int64_t(1) << 30) ? args.batch : (int64_t(1) << 30);
-  hipLaunchKernelGGL((expm_tile_kernel<T, P, Pair>), dim3(static_cast<unsigned>(grid)), dim3(64), 0, stream, args);
-  return hipGetLastError();
+  const int xl = load_class(args.x);
+  if constexpr (Pair) {
+    const int gl = load_class(args.g);
+    if (xl == kLoadRows) {
+      return gl == kLoadRows ? launch_tile_l<T, P, Pair, kLoadRows, kLoadRows>(args, stream)
+                             : launch_tile_l<T, P, Pair, kLoadRows, kLoadCols>(args, stream);
+    }
+    return gl == kLoadRows ? launch_tile_l<T, P, Pair, kLoadCols, kLoadRows>(args, stream)
+                           : launch_tile_l<T, P, Pair, kLoadCols, kLoadCols>(args, stream);
+  } else {
+    return xl == kLoadRows ? launch_tile_l<T, P, Pair, kLoadRows, kLoadRows>(args, stream)
+                           : launch_tile_l<T, P, Pair, kLoadCols, kLoadRows>(args, stream);
+  }
 }
 
 template <typename T, bool Pair>

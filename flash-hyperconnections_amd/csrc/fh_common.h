@@ -102,6 +102,14 @@ __device__ __forceinline__ float load_elem(const Operand& op, int64_t b, int r, 
   return to_f32<T>(p[b * op.sb + static_cast<int64_t>(r) * op.sr + static_cast<int64_t>(c) * op.sc]) * op.sign;
 }
 
+// Same without the view's sign (kernels that fold the sign into a later
+// exact multiply).
+template <typename T>
+__device__ __forceinline__ float load_elem_nosign(const Operand& op, int64_t b, int r, int c) {
+  const auto* p = static_cast<const typename T::storage*>(op.data);
+  return to_f32<T>(p[b * op.sb + static_cast<int64_t>(r) * op.sr + static_cast<int64_t>(c) * op.sc]);
+}
+
 template <typename T>
 __device__ __forceinline__ void store_elem(void* out, int64_t idx, float v) {
   static_cast<typename T::storage*>(out)[idx] = from_f32<T>(v);

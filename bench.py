@@ -180,6 +180,18 @@ def measure_config(name: str, torch, fh, steps: int, warmup: int, device) -> dic
     return out
 
 
+def profiled_traffic(key: str):
+    """HBM bytes per launch of a kernel from a committed rocprofv3 counter summary (or None)."""
+    path = ROOT / "profiles" / "expm_p4_c2_hbm_traffic.md"
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch " + key + " = "):
+                return int(line.rsplit("=", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_oracle_baseline(torch) -> dict:
     """The CPU restatement (scalar C, 1 thread) over the full config-2 workload."""
     import numpy as np
@@ -244,6 +256,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baselines")
     ap.add_argument("--only", default=None, help="comma list of configs (c2,c3,c4,c5,c5f32)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first run one device copy of exactly 64 MiB (profiler counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -258,6 +272,14 @@ def main() -> int:
     import flash_hypercons as fh
 
     device = torch.device("cuda:0")
+    if args.calibrate_copy:
+        # A plain copy of known size: reads and writes exactly 64 MiB.
+        src = torch.ones(16 << 20, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     configs = (args.only or "c2,c3,c4,c5,c5f32").split(",")
     results = {}
     for name in configs:
@@ -298,8 +320,9 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
-            "kernel": "expm_quad_kernel<F32, Pair=true> (Frechet backward, P=4)",
+            "traffic": profiled_traffic("expm_p4_frechet_c2_f32"),
+            "traffic_source": "profiles/expm_p4_c2_hbm_traffic.md (FETCH_SIZE, WRITE_SIZE; copy-calibrated)",
+            "kernel": "expm_p4_kernel<F32, Pair=true> (Frechet backward, P=4)",
             "algorithmic_bytes_per_launch": bytes_bwd,
             "mean_launch_ms": head["ms_bwd_kernel"],
         }

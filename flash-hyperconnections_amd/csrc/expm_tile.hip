@@ -5,21 +5,33 @@
 // Layout: a P x P matrix occupies R = P*P/64 VGPRs per lane in the MFMA
 // accumulator ("D") layout: lane l, VGPR r holds M[row(l, r)][l % P] with
 //   P = 16: row = 4*(l/16) + r
-//   P = 32: row = 8*(r/4) + 4*(l/32) + r%4.
-// Step r of a product feeds the A operand from VGPR r of X^T and the B operand
-// from VGPR r of Y; lane group g then contributes k = row(g, r), so the R
-// steps together cover k = 0..P-1 and
+//   P = 32: row = 8*(r/4) + 4*(l/32) + r%4,
+// i.e. row(l, r) = row0(l) + step(r).  Step r of a product feeds the A
+// operand from VGPR r of X^T and the B operand from VGPR r of Y; lane group g
+// then contributes k = row(g, r), so the R steps together cover k = 0..P-1 and
 //   X.Y = sum_r mfma(a = (X^T).v[r], b = Y.v[r])
 // needs no data movement for Y.  Left operands are transposed through a
-// padded LDS tile (P x (P+1) floats).
+// padded LDS tile (P x (P+1) floats); the workgroup is the one wavefront,
+// whose LDS accesses complete in issue order, so the transposes need
+// compiler ordering only, no barrier and no wait.
 //
 // The MFMA pipe and the VALU do not execute concurrently on gfx950, so every
-// VALU instruction adds to the MFMA time; the kernel keeps VALU work to the
-// combines, one transpose per left operand and the loads/stores.  It is
-// persistent: each wavefront walks matrices with a grid stride and issues the
-// next matrix's loads before computing the current one.  The evaluation
-// order keeps at most four powers and three temporaries live so that two
-// wavefronts fit per SIMD at P = 32.
+// VALU instruction adds to the MFMA time.  The kernel therefore keeps VALU
+// work to the combines:
+// * loads and stores go through buffer resources: one per-lane offset fixed
+//   for the whole kernel, the per-VGPR row offsets in scalar registers and
+//   the matrix base in the descriptor, so addressing costs no VALU;
+// * the next matrix's storage bits are prefetched into registers and only
+//   converted when its turn comes, so the prefetch never stalls;
+// * s comes from an FP32 estimate of the norm (a few adds and a cross-lane
+//   maximum) whenever that estimate decides it exactly; the FP64 sequential
+//   column sums of the reference run only near a squaring boundary or for
+//   non-finite input;
+// * products accumulate into the MFMA accumulator that already holds the
+//   term added to them (B4 into A9 = B1.B5 + B4, B2 into T = B2 + ..), and
+//   the Frechet half D1.U2 + U1.D2 is one accumulation chain.
+// Evaluation order therefore differs from the reference's sequential FMA
+// chains (parity is by tolerance; s is bit-identical).
 #include "fh_kernels.h"
 
 namespace fh {
@@ -35,8 +47,11 @@ template <>
 struct TileCfg<16> {
   static constexpr int R = 4;
   using acc_t = v4f;
-  __device__ static __forceinline__ int row(int lane, int r) { return 4 * (lane >> 4) + r; }
+  __device__ static constexpr int step(int r) { return r; }
+  __device__ static __forceinline__ int row0(int lane) { return 4 * (lane >> 4); }
   __device__ static __forceinline__ int col(int lane) { return lane & 15; }
+  // VGPR holding this lane's diagonal entry, -1 when it holds none.
+  __device__ static __forceinline__ int diag_reg(int lane) { return (lane >> 4) == ((lane & 15) >> 2) ? (lane & 3) : -1; }
   __device__ static __forceinline__ acc_t mfma(float a, float b, acc_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
   }
@@ -46,12 +61,20 @@ template <>
 struct TileCfg<32> {
   static constexpr int R = 16;
   using acc_t = v16f;
-  __device__ static __forceinline__ int row(int lane, int r) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+  __device__ static constexpr int step(int r) { return 8 * (r >> 2) + (r & 3); }
+  __device__ static __forceinline__ int row0(int lane) { return 4 * (lane >> 5); }
   __device__ static __forceinline__ int col(int lane) { return lane & 31; }
+  __device__ static __forceinline__ int diag_reg(int lane) {
+    const int c = lane & 31;
+    return ((c >> 2) & 1) == (lane >> 5) ? 4 * (c >> 3) + (c & 3) : -1;
+  }
   __device__ static __forceinline__ acc_t mfma(float a, float b, acc_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
   }
 };
+
+template <int P>
+using Acc = typename TileCfg<P>::acc_t;
 
 template <int P>
 struct Tm {
@@ -65,87 +88,113 @@ struct PTm {
 };
 
 template <int P>
-__device__ __forceinline__ Tm<P> mm(const Tm<P>& xt, const Tm<P>& y) {
-  using C = TileCfg<P>;
-  typename C::acc_t acc = {};
+__device__ __forceinline__ Acc<P> to_acc(const Tm<P>& m) {
+  Acc<P> a;
 #pragma unroll
-  for (int r = 0; r < C::R; ++r) acc = C::mfma(xt.v[r], y.v[r], acc);
-  Tm<P> out;
+  for (int r = 0; r < TileCfg<P>::R; ++r) a[r] = m.v[r];
+  return a;
+}
+template <int P>
+__device__ __forceinline__ Tm<P> from_acc(const Acc<P>& a) {
+  Tm<P> m;
 #pragma unroll
-  for (int r = 0; r < C::R; ++r) out.v[r] = acc[r];
+  for (int r = 0; r < TileCfg<P>::R; ++r) m.v[r] = a[r];
+  return m;
+}
+
+// acc + X.Y, X given as X^T in the D layout.
+template <int P>
+__device__ __forceinline__ Acc<P> mma(const Tm<P>& xt, const Tm<P>& y, Acc<P> acc) {
+#pragma unroll
+  for (int r = 0; r < TileCfg<P>::R; ++r) acc = TileCfg<P>::mfma(xt.v[r], y.v[r], acc);
+  return acc;
+}
+
+// (D1, U1).(D2, U2) + (Dc, Uc) = (D1.D2 + Dc, D1.U2 + U1.D2 + Uc).
+template <int P, bool Pair>
+__device__ __forceinline__ PTm<P, Pair> pmm(const PTm<P, Pair>& xt, const PTm<P, Pair>& y, const PTm<P, Pair>& c) {
+  PTm<P, Pair> out;
+  out.d = from_acc<P>(mma<P>(xt.d, y.d, to_acc<P>(c.d)));
+  if constexpr (Pair) out.u = from_acc<P>(mma<P>(xt.u, y.d, mma<P>(xt.d, y.u, to_acc<P>(c.u))));
+  return out;
+}
+template <int P, bool Pair>
+__device__ __forceinline__ PTm<P, Pair> pmm(const PTm<P, Pair>& xt, const PTm<P, Pair>& y) {
+  PTm<P, Pair> out;
+  const Acc<P> zero = {};
+  out.d = from_acc<P>(mma<P>(xt.d, y.d, zero));
+  if constexpr (Pair) out.u = from_acc<P>(mma<P>(xt.u, y.d, mma<P>(xt.d, y.u, zero)));
   return out;
 }
 
-template <int P>
-__device__ __forceinline__ Tm<P> tadd(const Tm<P>& a, const Tm<P>& b) {
-  Tm<P> c;
-#pragma unroll
-  for (int r = 0; r < TileCfg<P>::R; ++r) c.v[r] = a.v[r] + b.v[r];
-  return c;
+// Compiler ordering of the wavefront's LDS accesses (the hardware already
+// performs one wavefront's LDS operations in issue order).
+__device__ __forceinline__ void lds_order() {
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 }
 
-// D-layout of M -> D-layout of M^T through the wavefront's LDS tile.  The
-// workgroup is this one wavefront, so the barriers only order its own LDS
-// traffic.
 template <int P>
-__device__ __forceinline__ Tm<P> transpose(const Tm<P>& m, float* buf, int lane) {
+__device__ __forceinline__ void tile_write(const Tm<P>& m, float* buf, int lane) {
   using C = TileCfg<P>;
   constexpr int LD = P + 1;
   const int c = C::col(lane);
+  const int r0 = C::row0(lane);
 #pragma unroll
-  for (int r = 0; r < C::R; ++r) buf[C::row(lane, r) * LD + c] = m.v[r];
-  __syncthreads();
+  for (int r = 0; r < C::R; ++r) buf[(r0 + C::step(r)) * LD + c] = m.v[r];
+}
+template <int P>
+__device__ __forceinline__ Tm<P> tile_read_transposed(const float* buf, int lane) {
+  using C = TileCfg<P>;
+  constexpr int LD = P + 1;
+  const int c = C::col(lane);
+  const int r0 = C::row0(lane);
   Tm<P> t;
 #pragma unroll
-  for (int r = 0; r < C::R; ++r) t.v[r] = buf[c * LD + C::row(lane, r)];
-  __syncthreads();
+  for (int r = 0; r < C::R; ++r) t.v[r] = buf[c * LD + r0 + C::step(r)];
   return t;
 }
 
-template <int P, bool Pair>
-__device__ __forceinline__ PTm<P, Pair> pmm(const PTm<P, Pair>& xt, const PTm<P, Pair>& y) {
-  PTm<P, Pair> c;
-  c.d = mm<P>(xt.d, y.d);
-  if constexpr (Pair) c.u = tadd<P>(mm<P>(xt.d, y.u), mm<P>(xt.u, y.d));
-  return c;
-}
-template <int P, bool Pair>
-__device__ __forceinline__ PTm<P, Pair> padd(const PTm<P, Pair>& a, const PTm<P, Pair>& b) {
-  PTm<P, Pair> c;
-  c.d = tadd<P>(a.d, b.d);
-  if constexpr (Pair) c.u = tadd<P>(a.u, b.u);
-  return c;
-}
+// D layout of M -> D layout of M^T (both halves of a pair in one round).
 template <int P, bool Pair>
 __device__ __forceinline__ PTm<P, Pair> ptranspose(const PTm<P, Pair>& a, float* buf, int lane) {
-  PTm<P, Pair> c;
-  c.d = transpose<P>(a.d, buf, lane);
-  if constexpr (Pair) c.u = transpose<P>(a.u, buf, lane);
-  return c;
+  constexpr int T = P * (P + 1);
+  tile_write<P>(a.d, buf, lane);
+  if constexpr (Pair) tile_write<P>(a.u, buf + T, lane);
+  lds_order();
+  PTm<P, Pair> t;
+  t.d = tile_read_transposed<P>(buf, lane);
+  if constexpr (Pair) t.u = tile_read_transposed<P>(buf + T, lane);
+  lds_order();
+  return t;
 }
 
-// B(K+1) = c0*I + c1*A + c2*A^2 + c3*A^3 + c6*A^6 (csrc/MatrixExpSmall.cuh:
-// 268-281) with zero coefficients skipped; identity on D only.
-template <int K, int P, bool Pair>
+// base + B(K+1), B(K+1) = c0*I + c1*A + c2*A^2 + c3*A^3 + c6*A^6 (reference
+// csrc/MatrixExpSmall.cuh:268-281); zero coefficients skipped, identity on D
+// only (`dreg`: the VGPR of this lane's diagonal entry, -1 for none).
+template <int K, int P, bool Pair, bool Base>
 __device__ __forceinline__ PTm<P, Pair> combine(const PTm<P, Pair>& a, const PTm<P, Pair>& a2,
                                                 const PTm<P, Pair>& a3, const PTm<P, Pair>& a6,
-                                                const float (&diag)[TileCfg<P>::R]) {
+                                                const PTm<P, Pair>& base, int dreg) {
+  using C = TileCfg<P>;
   constexpr float c0 = kCoef[K][0], c1 = kCoef[K][1], c2 = kCoef[K][2], c3 = kCoef[K][3], c6 = kCoef[K][4];
   PTm<P, Pair> b;
 #pragma unroll
-  for (int r = 0; r < TileCfg<P>::R; ++r) {
-    float t;
-    if constexpr (c1 != 0.f) {
-      t = __builtin_fmaf(c1, a.d.v[r], c0 * diag[r]);
-    } else {
-      t = c0 * diag[r];
+  for (int r = 0; r < C::R; ++r) {
+    float t = Base ? base.d.v[r] : 0.f;
+    if constexpr (c0 != 0.f) {
+      const float id = dreg == r ? c0 : 0.f;
+      t = Base ? t + id : id;
     }
+    if constexpr (c1 != 0.f) t = __builtin_fmaf(c1, a.d.v[r], t);
     t = __builtin_fmaf(c2, a2.d.v[r], t);
     t = __builtin_fmaf(c3, a3.d.v[r], t);
     if constexpr (c6 != 0.f) t = __builtin_fmaf(c6, a6.d.v[r], t);
     b.d.v[r] = t;
     if constexpr (Pair) {
-      float w = (c1 != 0.f) ? __builtin_fmaf(c2, a2.u.v[r], c1 * a.u.v[r]) : c2 * a2.u.v[r];
+      float w = Base ? base.u.v[r] : 0.f;
+      if constexpr (c1 != 0.f) w = __builtin_fmaf(c1, a.u.v[r], w);
+      w = __builtin_fmaf(c2, a2.u.v[r], w);
       w = __builtin_fmaf(c3, a3.u.v[r], w);
       if constexpr (c6 != 0.f) w = __builtin_fmaf(c6, a6.u.v[r], w);
       b.u.v[r] = w;
@@ -154,115 +203,215 @@ __device__ __forceinline__ PTm<P, Pair> combine(const PTm<P, Pair>& a, const PTm
   return b;
 }
 
-// Layout classes for loading: rows contiguous (sc == 1) loads the D layout of
-// the matrix itself; columns contiguous (sr == 1) loads the D layout of its
-// transpose; anything else gathers element-wise through the strides.
+// Layout classes for loading: rows contiguous (kLoadRows) loads the D layout
+// of the matrix itself; columns contiguous (kLoadCols) loads the D layout of
+// its transpose.  Either works for any strides; the class only decides which
+// of the two layouts comes from memory and which from the LDS transpose.
 constexpr int kLoadRows = 0;
 constexpr int kLoadCols = 1;
 
+// Byte addressing of one operand in the D layout of the loaded matrix: the
+// matrix base goes into the descriptor, `lane_off` is this lane's offset for
+// VGPR 0 and step(r) * `major` the uniform offset of VGPR r.
+struct TileSrc {
+  const char* data;
+  int64_t sb;        // bytes per batch step
+  int32_t major;     // bytes per D-layout row step
+  int32_t lane_off;  // bytes, VGPR 0 of this lane
+  uint32_t records;  // footprint of one matrix in bytes
+};
+
 template <typename T, int P>
-__device__ __forceinline__ Tm<P> load_tile(const Operand& op, int64_t b, int n, int lane, bool transposed) {
+__device__ __forceinline__ TileSrc make_src(const Operand& op, int layout, int n, int lane) {
   using C = TileCfg<P>;
-  const int c = C::col(lane);
+  constexpr int es = ElemIO<T>::bytes;
+  const int64_t major = layout == kLoadCols ? op.sc : op.sr;
+  const int64_t minor = layout == kLoadCols ? op.sr : op.sc;
+  TileSrc s;
+  s.data = static_cast<const char*>(op.data);
+  s.sb = op.sb * es;
+  s.major = static_cast<int32_t>(major * es);
+  s.lane_off = static_cast<int32_t>((C::row0(lane) * major + C::col(lane) * minor) * es);
+  s.records = static_cast<uint32_t>(((n - 1) * (op.sr + op.sc) + 1) * es);
+  return s;
+}
+
+template <typename T, int P>
+struct RawTile {
+  typename ElemIO<T>::raw_t v[TileCfg<P>::R];
+};
+
+// Storage bits of matrix b; entries outside the n x n block read as +0.
+template <typename T, int P, bool Full>
+__device__ __forceinline__ RawTile<T, P> load_raw(const TileSrc& s, int64_t b, int n, int lane) {
+  using C = TileCfg<P>;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(s.data + b * s.sb, s.records);
+  RawTile<T, P> t;
+  if constexpr (Full) {
+#pragma unroll
+    for (int r = 0; r < C::R; ++r) t.v[r] = ElemIO<T>::load(rs, s.lane_off, C::step(r) * s.major);
+  } else {
+    const bool col_ok = C::col(lane) < n;
+#pragma unroll
+    for (int r = 0; r < C::R; ++r) {
+      const bool ok = col_ok && C::row0(lane) + C::step(r) < n;
+      t.v[r] = ElemIO<T>::load(rs, ok ? s.lane_off + C::step(r) * s.major : kOutOfRange, 0);
+    }
+  }
+  return t;
+}
+
+template <typename T, int P>
+__device__ __forceinline__ Tm<P> to_tile(const RawTile<T, P>& raw) {
   Tm<P> m;
 #pragma unroll
-  for (int r = 0; r < C::R; ++r) {
-    const int row = C::row(lane, r);
-    const bool in = row < n && c < n;
-    // transposed: element (row, c) of M^T, i.e. M[c][row]
-    m.v[r] = in ? load_elem_nosign<T>(op, b, transposed ? c : row, transposed ? row : c) : 0.f;
-  }
+  for (int r = 0; r < TileCfg<P>::R; ++r) m.v[r] = ElemIO<T>::value(raw.v[r]);
   return m;
+}
+
+// Contiguous [batch, n, n] output in the input dtype.
+template <typename T, int P, bool Full>
+__device__ __forceinline__ void store_tile(void* out, int64_t b, int n, int lane, const Tm<P>& m) {
+  using C = TileCfg<P>;
+  constexpr int es = ElemIO<T>::bytes;
+  const int64_t nn = static_cast<int64_t>(n) * n;
+  const __amdgpu_buffer_rsrc_t rs =
+      make_rsrc(static_cast<char*>(out) + b * nn * es, static_cast<uint32_t>(nn * es));
+  const int32_t lane_off = (C::row0(lane) * n + C::col(lane)) * es;
+  if constexpr (Full) {
+#pragma unroll
+    for (int r = 0; r < C::R; ++r) ElemIO<T>::store(m.v[r], rs, lane_off + C::step(r) * P * es, 0);
+  } else {
+    const bool col_ok = C::col(lane) < n;
+#pragma unroll
+    for (int r = 0; r < C::R; ++r) {
+      const bool ok = col_ok && C::row0(lane) + C::step(r) < n;
+      ElemIO<T>::store(m.v[r], rs, ok ? lane_off + C::step(r) * n * es : kOutOfRange, 0);
+    }
+  }
+}
+
+// Maximum over the lanes of a row of 16 (every lane of the row gets it).
+__device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
+  v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xB1, 0xF, 0xF, false)));
+  v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x4E, 0xF, 0xF, false)));
+  v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x141, 0xF, 0xF, false)));
+  v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x140, 0xF, 0xF, false)));
+  return v;
+}
+
+// FP32 estimate of the 1-norm max_j sum_i |A[i][j]| (+ |G[i][j]|) from the D
+// layout of A (and G): each lane sums its column entries, the lanes sharing a
+// column add up, and the column maximum is taken on the bit patterns (equal
+// order for non-negative floats; NaN and inf compare above every finite
+// value).  Relative error at most (2R + 2) * 2^-24 < 2^-18.
+template <int P, bool Pair>
+__device__ __forceinline__ float norm_estimate(const PTm<P, Pair>& a) {
+  float p = 0.f;
+#pragma unroll
+  for (int r = 0; r < TileCfg<P>::R; ++r) {
+    p += __builtin_fabsf(a.d.v[r]);
+    if constexpr (Pair) p += __builtin_fabsf(a.u.v[r]);
+  }
+  if constexpr (P == 16) p += __shfl_xor(p, 16);
+  p += __shfl_xor(p, 32);
+  uint32_t m = row_max_u32(__float_as_uint(p) & 0x7FFFFFFFu);
+  uint32_t top = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m), 0));
+  if constexpr (P == 32) top = max(top, static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m), 16)));
+  return __uint_as_float(top);
+}
+
+// The reference's FP64 norm (csrc/MatrixExpSmall.cuh:343-357): per column the
+// rows summed sequentially, |A| then |G| per row, then the column maximum; the
+// total of the column sums is finite exactly when every entry is (non-finite
+// rule, :318-331).  Returns false for non-finite input.
+template <int P, bool Pair>
+__device__ __forceinline__ bool exact_squarings(const PTm<P, Pair>& a, float* buf, double* colsum,
+                                                          int lane, int& s) {
+  constexpr int LD = P + 1;
+  tile_write<P>(a.d, buf, lane);
+  if constexpr (Pair) tile_write<P>(a.u, buf + P * LD, lane);
+  lds_order();
+  if (lane < P) {
+    double v = 0.;
+    for (int row = 0; row < P; ++row) {
+      v += fabs(static_cast<double>(buf[row * LD + lane]));
+      if constexpr (Pair) v += fabs(static_cast<double>(buf[P * LD + row * LD + lane]));
+    }
+    colsum[lane] = v;
+  }
+  lds_order();
+  double norm = 0., total = 0.;
+  for (int j = 0; j < P; ++j) {
+    norm = fmax(norm, colsum[j]);
+    total += colsum[j];
+  }
+  lds_order();
+  if (!__builtin_isfinite(total)) return false;
+  s = squarings_from_norm(norm);
+  return true;
 }
 
 // Occupancy target (wavefronts per SIMD) the register allocation must meet.
 template <int P, bool Pair>
 constexpr int kTileWaves() {
-  return P == 16 ? 4 : (Pair ? 1 : 2);
+  return P == 16 ? 4 : (Pair ? 2 : 3);
 }
 
-template <typename T, int P, bool Pair, int XL, int GL>
+template <typename T, int P, bool Pair, int XL, int GL, bool Full>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kTileWaves<P, Pair>(), 8))) void expm_tile_kernel(
     ExpmArgs args) {
   using C = TileCfg<P>;
   constexpr int R = C::R;
-  constexpr int LD = P + 1;
-  __shared__ float buf[2 * P * LD];
+  __shared__ float buf[2 * P * (P + 1)];
   __shared__ double colsum[P];
   const int lane = threadIdx.x;
-  const int c = C::col(lane);
-  const int n = args.n;
-  float diag[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) diag[r] = (C::row(lane, r) == c) ? 1.f : 0.f;
+  const int n = Full ? P : args.n;
+  const TileSrc sx = make_src<T, P>(args.x, XL, n, lane);
+  const TileSrc sg = make_src<T, P>(args.g, GL, n, lane);
 
   int64_t b = blockIdx.x;
-  Tm<P> nx, ng;
+  RawTile<T, P> nx, ng;
   if (b < args.batch) {
-    nx = load_tile<T, P>(args.x, b, n, lane, XL == kLoadCols);
-    if constexpr (Pair) ng = load_tile<T, P>(args.g, b, n, lane, GL == kLoadCols);
+    nx = load_raw<T, P, Full>(sx, b, n, lane);
+    if constexpr (Pair) ng = load_raw<T, P, Full>(sg, b, n, lane);
   }
+  const int dreg_lane = C::diag_reg(lane);
   for (; b < args.batch; b += gridDim.x) {
-    const Tm<P> lx = nx;
+    // Opaque per matrix so that the identity terms are selected where they
+    // are used instead of being kept live as 2R registers across the loop.
+    int dreg = dreg_lane;
+    asm volatile("" : "+v"(dreg));
+    const Tm<P> lx = to_tile<T, P>(nx);
     Tm<P> lg;
-    if constexpr (Pair) lg = ng;
+    if constexpr (Pair) lg = to_tile<T, P>(ng);
     if (b + gridDim.x < args.batch) {
-      nx = load_tile<T, P>(args.x, b + gridDim.x, n, lane, XL == kLoadCols);
-      if constexpr (Pair) ng = load_tile<T, P>(args.g, b + gridDim.x, n, lane, GL == kLoadCols);
+      nx = load_raw<T, P, Full>(sx, b + gridDim.x, n, lane);
+      if constexpr (Pair) ng = load_raw<T, P, Full>(sg, b + gridDim.x, n, lane);
     }
 
-    // Both layouts of X (and G) through the LDS tile; the tile that holds the
-    // plain layout also feeds the column sums of the norm.
+    // Both layouts of X (and G): the loaded one and its LDS transpose.
     PTm<P, Pair> a, at;
-    if constexpr (XL == kLoadCols) {
-      at.d = lx;
-      a.d = transpose<P>(lx, buf, lane);
-    } else {
-      a.d = lx;
-      at.d = transpose<P>(lx, buf, lane);
-    }
-    if constexpr (Pair) {
-      if constexpr (GL == kLoadCols) {
-        at.u = lg;
-        a.u = transpose<P>(lg, buf, lane);
-      } else {
-        a.u = lg;
-        at.u = transpose<P>(lg, buf, lane);
+    {
+      PTm<P, Pair> loaded;
+      loaded.d = lx;
+      if constexpr (Pair) loaded.u = lg;
+      const PTm<P, Pair> other = ptranspose<P, Pair>(loaded, buf, lane);
+      a.d = XL == kLoadCols ? other.d : lx;
+      at.d = XL == kLoadCols ? lx : other.d;
+      if constexpr (Pair) {
+        a.u = GL == kLoadCols ? other.u : lg;
+        at.u = GL == kLoadCols ? lg : other.u;
       }
     }
-    // FP64 1-norm, rows summed sequentially per column, |A| then |G| per row
-    // (csrc/MatrixExpSmall.cuh:343-357); the total of the column sums is
-    // finite exactly when every entry is (non-finite rule, :318-331).
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      buf[C::row(lane, r) * LD + c] = a.d.v[r];
-      if constexpr (Pair) buf[P * LD + C::row(lane, r) * LD + c] = a.u.v[r];
-    }
-    __syncthreads();
-    if (lane < P) {
-      double v = 0.;
-      for (int row = 0; row < P; ++row) {
-        v += fabs(static_cast<double>(buf[row * LD + lane]));
-        if constexpr (Pair) v += fabs(static_cast<double>(buf[P * LD + row * LD + lane]));
-      }
-      colsum[lane] = v;
-    }
-    __syncthreads();
-    double norm = 0., total = 0.;
-    for (int j = 0; j < P; ++j) {
-      norm = fmax(norm, colsum[j]);
-      total += colsum[j];
-    }
-    const bool bad = !__builtin_isfinite(total);
-    const int s = bad ? 0 : squarings_from_norm(norm);
-    __syncthreads();
 
-    if (bad) {
+    int s;
+    if (!squarings_from_estimate(norm_estimate<P, Pair>(a), s) && !exact_squarings<P, Pair>(a, buf, colsum, lane, s)) {
+      // Non-finite entry: the whole matrix is NaN (csrc/MatrixExpSmall.cuh:318-331).
+      Tm<P> nan;
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int row = C::row(lane, r);
-        if (row < n && c < n) store_elem<T>(args.out, (b * n + row) * n + c, __builtin_nanf(""));
-      }
+      for (int r = 0; r < R; ++r) nan.v[r] = __builtin_nanf("");
+      store_tile<T, P, Full>(args.out, b, n, lane, nan);
       if (lane == 0 && args.s_out) args.s_out[b] = -1;
       continue;
     }
@@ -282,57 +431,56 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kTileWaves<P
       }
     }
 
-    // Degree-18 polynomial.  Powers are formed as A.A and A.A^2 (all factors
-    // are polynomials in the same matrix), then A^6 = A^3.A^3,
-    // A9 = B1.B5 + B4 and T = B2 + (B3 + A9).A9.
+    // Degree-18 polynomial (csrc/MatrixExpSmall.cuh:83-106): A^2 = A.A,
+    // A^3 = A.A^2, A^6 = A^3.A^3, A9 = B1.B5 + B4, T = B2 + (B3 + A9).A9.
     const PTm<P, Pair> a2 = pmm<P, Pair>(at, a);
     const PTm<P, Pair> a3 = pmm<P, Pair>(at, a2);
     const PTm<P, Pair> a6 = pmm<P, Pair>(ptranspose<P, Pair>(a3, buf, lane), a3);
-    PTm<P, Pair> a9 = pmm<P, Pair>(ptranspose<P, Pair>(combine<0, P, Pair>(a, a2, a3, a6, diag), buf, lane),
-                                   combine<4, P, Pair>(a, a2, a3, a6, diag));
-    a9 = padd<P, Pair>(a9, combine<3, P, Pair>(a, a2, a3, a6, diag));
-    const PTm<P, Pair> lhst =
-        ptranspose<P, Pair>(padd<P, Pair>(combine<2, P, Pair>(a, a2, a3, a6, diag), a9), buf, lane);
-    const PTm<P, Pair> b2 = combine<1, P, Pair>(a, a2, a3, a6, diag);
-    PTm<P, Pair> res = padd<P, Pair>(b2, pmm<P, Pair>(lhst, a9));
+    const PTm<P, Pair> none{};
+    PTm<P, Pair> a9 = pmm<P, Pair>(ptranspose<P, Pair>(combine<0, P, Pair, false>(a, a2, a3, a6, none, dreg), buf, lane),
+                                   combine<4, P, Pair, false>(a, a2, a3, a6, none, dreg),
+                                   combine<3, P, Pair, false>(a, a2, a3, a6, none, dreg));
+    const PTm<P, Pair> lhst = ptranspose<P, Pair>(combine<2, P, Pair, true>(a, a2, a3, a6, a9, dreg), buf, lane);
+    PTm<P, Pair> res = pmm<P, Pair>(lhst, a9, combine<1, P, Pair, false>(a, a2, a3, a6, none, dreg));
     for (int i = 0; i < s; ++i) res = pmm<P, Pair>(ptranspose<P, Pair>(res, buf, lane), res);
 
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int row = C::row(lane, r);
-      if (row < n && c < n) store_elem<T>(args.out, (b * n + row) * n + c, Pair ? res.u.v[r] : res.d.v[r]);
-    }
+    store_tile<T, P, Full>(args.out, b, n, lane, Pair ? res.u : res.d);
     if (lane == 0 && args.s_out) args.s_out[b] = s;
   }
 }
 
-template <typename T, int P, bool Pair, int XL, int GL>
+template <typename T, int P, bool Pair, int XL, int GL, bool Full>
 hipError_t launch_tile_l(const ExpmArgs& args, hipStream_t stream) {
   static const int64_t resident =
-      resident_blocks(reinterpret_cast<const void*>(&expm_tile_kernel<T, P, Pair, XL, GL>), 64);
+      resident_blocks(reinterpret_cast<const void*>(&expm_tile_kernel<T, P, Pair, XL, GL, Full>), 64);
   const int64_t grid = args.batch < resident ? args.batch : resident;
-  hipLaunchKernelGGL((expm_tile_kernel<T, P, Pair, XL, GL>), dim3(static_cast<unsigned>(grid)), dim3(64), 0, stream,
-                     args);
+  hipLaunchKernelGGL((expm_tile_kernel<T, P, Pair, XL, GL, Full>), dim3(static_cast<unsigned>(grid)), dim3(64), 0,
+                     stream, args);
   return hipGetLastError();
 }
 
 int load_class(const Operand& op) { return (op.sr == 1 && op.sc != 1) ? kLoadCols : kLoadRows; }
 
-template <typename T, int P, bool Pair>
-hipError_t launch_tile_tp(const ExpmArgs& args, hipStream_t stream) {
+template <typename T, int P, bool Pair, bool Full>
+hipError_t launch_tile_f(const ExpmArgs& args, hipStream_t stream) {
   const int xl = load_class(args.x);
   if constexpr (Pair) {
     const int gl = load_class(args.g);
     if (xl == kLoadRows) {
-      return gl == kLoadRows ? launch_tile_l<T, P, Pair, kLoadRows, kLoadRows>(args, stream)
-                             : launch_tile_l<T, P, Pair, kLoadRows, kLoadCols>(args, stream);
+      return gl == kLoadRows ? launch_tile_l<T, P, Pair, kLoadRows, kLoadRows, Full>(args, stream)
+                             : launch_tile_l<T, P, Pair, kLoadRows, kLoadCols, Full>(args, stream);
     }
-    return gl == kLoadRows ? launch_tile_l<T, P, Pair, kLoadCols, kLoadRows>(args, stream)
-                           : launch_tile_l<T, P, Pair, kLoadCols, kLoadCols>(args, stream);
+    return gl == kLoadRows ? launch_tile_l<T, P, Pair, kLoadCols, kLoadRows, Full>(args, stream)
+                           : launch_tile_l<T, P, Pair, kLoadCols, kLoadCols, Full>(args, stream);
   } else {
-    return xl == kLoadRows ? launch_tile_l<T, P, Pair, kLoadRows, kLoadRows>(args, stream)
-                           : launch_tile_l<T, P, Pair, kLoadCols, kLoadRows>(args, stream);
+    return xl == kLoadRows ? launch_tile_l<T, P, Pair, kLoadRows, kLoadRows, Full>(args, stream)
+                           : launch_tile_l<T, P, Pair, kLoadCols, kLoadRows, Full>(args, stream);
   }
+}
+
+template <typename T, int P, bool Pair>
+hipError_t launch_tile_tp(const ExpmArgs& args, hipStream_t stream) {
+  return args.n == P ? launch_tile_f<T, P, Pair, true>(args, stream) : launch_tile_f<T, P, Pair, false>(args, stream);
 }
 
 template <typename T, bool Pair>
@@ -340,9 +488,21 @@ hipError_t launch_tile_t(const ExpmArgs& args, int P, hipStream_t stream) {
   return P == 16 ? launch_tile_tp<T, 16, Pair>(args, stream) : launch_tile_tp<T, 32, Pair>(args, stream);
 }
 
+// Buffer addressing needs non-negative in-matrix strides and a per-matrix
+// footprint below 2^31 bytes.
+bool addressable(const Operand& op, int n, int es) {
+  if (op.sr < 0 || op.sc < 0) return false;
+  const int64_t limit = (int64_t{1} << 31) / es;
+  if (op.sr >= limit || op.sc >= limit) return false;
+  return (n - 1) * (op.sr + op.sc) + 1 < limit;
+}
+
 }  // namespace
 
 hipError_t launch_tile(const ExpmArgs& args, int dtype, int P, bool pair, hipStream_t stream) {
+  const int es = dtype == F32::code ? 4 : 2;
+  if (!addressable(args.x, args.n, es) || (pair && !addressable(args.g, args.n, es)))
+    return launch_generic(args, dtype, P, pair, stream);
   if (dtype == F32::code) return pair ? launch_tile_t<F32, true>(args, P, stream) : launch_tile_t<F32, false>(args, P, stream);
   if (dtype == BF16::code) return pair ? launch_tile_t<BF16, true>(args, P, stream) : launch_tile_t<BF16, false>(args, P, stream);
   return pair ? launch_tile_t<F16, true>(args, P, stream) : launch_tile_t<F16, false>(args, P, stream);

@@ -134,6 +134,79 @@ __device__ __forceinline__ int squarings_from_norm(double norm) {
   return e;
 }
 
+// s from an FP32 estimate of the norm whose relative error is below 2^-18.
+// s(norm) is monotone and steps only where norm / theta18 crosses a power of
+// two, so when the estimate keeps q = norm / theta18 at least 2^-15 (relative)
+// away from every power of two, the exact FP64 norm lies on the same step and
+// has the same s.  Returns false -- only the exact norm can decide -- inside
+// those bands and for huge or non-finite estimates.
+__device__ __forceinline__ bool squarings_from_estimate(float norm, int& s) {
+  if (!(norm < 0x1p120f)) return false;
+  constexpr float kInvTheta = static_cast<float>(1.0 / kTheta18);
+  const float q = norm * kInvTheta;
+  if (q <= 0.5f) {
+    s = 0;
+    return true;
+  }
+  int e;
+  const float m = __builtin_frexpf(q, &e);
+  if (m < 0.5f + 0x1p-16f || m > 1.f - 0x1p-16f) return false;
+  s = e > 0 ? e : 0;
+  return true;
+}
+
+// Raw buffer resource over `bytes` bytes at `base` (gfx9 descriptor word 3).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                           0x00020000);
+}
+
+// An offset no footprint reaches: buffer loads there return 0, stores drop.
+constexpr int32_t kOutOfRange = static_cast<int32_t>(0x80000000u);
+
+// Element I/O through a buffer resource, keeping the storage bits (`raw_t`)
+// separate from the conversion so that a prefetch never waits for its data.
+template <typename T>
+struct ElemIO;
+template <>
+struct ElemIO<F32> {
+  using raw_t = uint32_t;
+  static constexpr int bytes = 4;
+  __device__ static __forceinline__ raw_t load(__amdgpu_buffer_rsrc_t rs, int32_t voff, int32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(rs, voff, soff, 0);
+  }
+  __device__ static __forceinline__ float value(raw_t v) { return __uint_as_float(v); }
+  __device__ static __forceinline__ void store(float v, __amdgpu_buffer_rsrc_t rs, int32_t voff, int32_t soff) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rs, voff, soff, 0);
+  }
+};
+template <>
+struct ElemIO<F16> {
+  using raw_t = uint16_t;
+  static constexpr int bytes = 2;
+  __device__ static __forceinline__ raw_t load(__amdgpu_buffer_rsrc_t rs, int32_t voff, int32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b16(rs, voff, soff, 0);
+  }
+  __device__ static __forceinline__ float value(raw_t v) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, v));
+  }
+  __device__ static __forceinline__ void store(float v, __amdgpu_buffer_rsrc_t rs, int32_t voff, int32_t soff) {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, from_f32<F16>(v)), rs, voff, soff, 0);
+  }
+};
+template <>
+struct ElemIO<BF16> {
+  using raw_t = uint16_t;
+  static constexpr int bytes = 2;
+  __device__ static __forceinline__ raw_t load(__amdgpu_buffer_rsrc_t rs, int32_t voff, int32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b16(rs, voff, soff, 0);
+  }
+  __device__ static __forceinline__ float value(raw_t v) { return to_f32<BF16>(v); }
+  __device__ static __forceinline__ void store(float v, __amdgpu_buffer_rsrc_t rs, int32_t voff, int32_t soff) {
+    __builtin_amdgcn_raw_buffer_store_b16(from_f32<BF16>(v), rs, voff, soff, 0);
+  }
+};
+
 __device__ __forceinline__ bool finite_f32(float v) { return __builtin_isfinite(v); }
 
 }  // namespace fh

@@ -3,12 +3,23 @@
 //
 // Each lane keeps its whole 4 x 4 matrix (16 VGPRs; the Frechet kernel keeps
 // the D and U blocks, 32 VGPRs) and every product is 64 plain FP32 FMAs with
-// compile-time register indices -- no cross-lane traffic, no transposes.  On
-// gfx950 a 64-lane FP32 FMA issues every 2 cycles (the same rate as the 4x4x1
-// MFMA, which cannot overlap with VALU work), while DPP-sourced operands run
-// at half rate, so this layout is the one that reaches the FMA floor.  The
-// per-matrix scalar work (FP64 norm, squaring count, scaling) is also done
-// once per matrix rather than once per row.
+// compile-time register indices -- no cross-lane traffic, no transposes.  The
+// per-matrix scalar work (norm, squaring count, scaling) is done once per
+// matrix rather than once per row.
+//
+// Measured on gfx950: a wave64 FP32 VALU instruction issues every ~3.3 cycles
+// at 2 wavefronts per SIMD and ~2.6 at 4; a 4x4x1 FP32 MFMA does 256 FMAs in
+// ~8.6 cycles but never overlaps VALU work, so a matrix-core variant (16
+// matrices per wavefront, LDS transposes for left operands) has the same
+// pipe-time floor and ran slower; DPP-sourced operands run at half rate.  The
+// Frechet kernel is VALU-bound at 2 wavefronts per SIMD (~190 VGPRs); the
+// forward kernel runs 4 per SIMD and is bound by memory plus its polynomial.
+//
+// Loads keep raw storage bytes until the group's turn.  Dense operands (64
+// packed matrices form one contiguous block) are read with 1 KB per load
+// instruction and routed to their lanes through LDS; other vector-class
+// operands load their rows or columns per lane; anything else element-wise.
+// Stores go through an LDS staging tile so that they are coalesced as well.
 //
 // Arithmetic is the reference's, element by element (csrc/MatrixExpSmall.cuh:
 // 22-106): product entries accumulate k = 0..3 with fmaf from +0, Frechet U
@@ -173,6 +184,119 @@ __device__ __forceinline__ M4 load_matrix(const Operand& op, int64_t b, int n, b
   return m;
 }
 
+// Raw storage bytes of one lane's matrix for the vector classes, in the
+// memory order of the class (row-major for kVecRows, column-major for
+// kVecCols); they are converted only when the group's turn comes, so a
+// prefetch never waits for its data.
+template <typename T>
+struct RawMat {
+  static constexpr int kWords = 4 * static_cast<int>(sizeof(typename T::storage));  // 16 or 8
+  uint32_t w[kWords];
+};
+
+// The four row (column) vectors of matrix b.
+template <typename T, int L>
+__device__ __forceinline__ RawMat<T> load_lane_raw(const Operand& op, int64_t b, bool valid) {
+  using S = typename T::storage;
+  RawMat<T> r;
+#pragma unroll
+  for (int k = 0; k < RawMat<T>::kWords; ++k) r.w[k] = 0u;
+  if (!valid) return r;
+  const S* base = static_cast<const S*>(op.data) + b * op.sb;
+  const int64_t step = L == kVecRows ? op.sr : op.sc;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    if constexpr (sizeof(S) == 4) {
+      const uint4 x = *reinterpret_cast<const uint4*>(base + v * step);
+      r.w[4 * v] = x.x;
+      r.w[4 * v + 1] = x.y;
+      r.w[4 * v + 2] = x.z;
+      r.w[4 * v + 3] = x.w;
+    } else {
+      const uint2 x = *reinterpret_cast<const uint2*>(base + v * step);
+      r.w[2 * v] = x.x;
+      r.w[2 * v + 1] = x.y;
+    }
+  }
+  return r;
+}
+
+// A full group of a dense operand: this lane's share of the group's
+// contiguous block, 16-byte chunks lane, lane + 64, ... -- each load
+// instruction reads 1 KB of consecutive memory.
+template <typename T>
+__device__ __forceinline__ RawMat<T> load_dense_raw(const Operand& op, int64_t group, int lane) {
+  using S = typename T::storage;
+  constexpr int C = RawMat<T>::kWords / 4;
+  const uint4* base = reinterpret_cast<const uint4*>(static_cast<const S*>(op.data) + group * 64 * 16);
+  RawMat<T> r;
+#pragma unroll
+  for (int q = 0; q < C; ++q) {
+    const uint4 x = base[q * 64 + lane];
+    r.w[4 * q] = x.x;
+    r.w[4 * q + 1] = x.y;
+    r.w[4 * q + 2] = x.z;
+    r.w[4 * q + 3] = x.w;
+  }
+  return r;
+}
+
+// Compiler ordering of the wavefront's LDS accesses (the hardware performs
+// one wavefront's LDS operations in issue order).
+__device__ __forceinline__ void lds_order() {
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Routes a dense group's chunks through the wavefront's LDS tile so that each
+// lane ends up with its own matrix: chunk c of matrix m goes to byte
+// c * 1040 + 16 * m (rows of 64 chunks padded by 16 bytes, so that both the
+// scattered writes and the per-lane reads are free of bank conflicts).
+constexpr int kDenseRowBytes = 1024 + 16;
+
+template <typename T>
+__device__ __forceinline__ void dense_to_lane(RawMat<T>& r, float* tile, int lane) {
+  constexpr int C = RawMat<T>::kWords / 4;
+  char* t = reinterpret_cast<char*>(tile);
+#pragma unroll
+  for (int q = 0; q < C; ++q) {
+    const int g = q * 64 + lane;
+    *reinterpret_cast<uint4*>(t + (g % C) * kDenseRowBytes + 16 * (g / C)) =
+        make_uint4(r.w[4 * q], r.w[4 * q + 1], r.w[4 * q + 2], r.w[4 * q + 3]);
+  }
+  lds_order();
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const uint4 x = *reinterpret_cast<const uint4*>(t + c * kDenseRowBytes + 16 * lane);
+    r.w[4 * c] = x.x;
+    r.w[4 * c + 1] = x.y;
+    r.w[4 * c + 2] = x.z;
+    r.w[4 * c + 3] = x.w;
+  }
+  lds_order();
+}
+
+// Row-major FP32 matrix (without the view's sign) from the raw bytes.
+template <typename T, int L>
+__device__ __forceinline__ M4 decode(const RawMat<T>& r) {
+  using S = typename T::storage;
+  M4 m;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    float v;
+    if constexpr (sizeof(S) == 4) {
+      v = __uint_as_float(r.w[e]);
+    } else {
+      const uint16_t h = static_cast<uint16_t>(r.w[e >> 1] >> (16 * (e & 1)));
+      v = to_f32<T>(__builtin_bit_cast(S, h));
+    }
+    // Memory order: rows class e = 4 * row + col, columns class e = 4 * col + row.
+    m.v[L == kVecRows ? e : 4 * (e & 3) + (e >> 2)] = v;
+  }
+  return m;
+}
+
 template <typename T, bool Full>
 __device__ __forceinline__ void store_matrix(void* out, int64_t b, int n, const M4& m) {
   using S = typename T::storage;
@@ -200,6 +324,12 @@ __device__ __forceinline__ void store_matrix(void* out, int64_t b, int n, const 
 
 constexpr int kP4Waves = 4;  // wavefronts per workgroup
 constexpr int kStageStride = 17;  // floats per matrix in the LDS staging tile (odd: conflict-free)
+
+// Per-wavefront LDS tile: the store staging area and, in turn, one (forward)
+// or two (Frechet: X and G) dense-group routing areas of 4 x 1040 bytes.
+template <bool Pair>
+constexpr int kTileFloats = (Pair ? 2 : 1) * kDenseRowBytes > 64 * kStageStride ? (Pair ? 2 : 1) * kDenseRowBytes
+                                                                                : 64 * kStageStride;
 
 // Stores the 64 matrices of a full group (n == 4, all rows valid) through
 // the wavefront's LDS tile so that the global stores are coalesced: lane l
@@ -231,15 +361,29 @@ __device__ __forceinline__ void store_group_staged(void* out, int64_t first, int
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 }
 
-// The whole pipeline for the matrix of this lane.
-template <typename T, bool Pair, int XL>
-__device__ __forceinline__ void compute_matrix(const ExpmArgs& args, PM<Pair> a, int64_t b, int n, bool valid,
-                                               int lane, bool full_group, float* tile) {
-  // FP64 1-norm: column sums over rows as ((x0 + x2) + (x1 + x3)) with
-  // x_r = |A[r][j]| (+ |G[r][j]|), the reference's butterfly order
-  // (csrc/MatrixExpSmall.cuh:144-152).  The sum of the column sums is finite
-  // exactly when every entry is: the non-finite rule of
-  // csrc/MatrixExpSmall.cuh:126-140.
+// Squaring count of this lane's matrix, or -1 for a non-finite one.  An FP32
+// estimate of the column-sum norm decides s whenever it lies clear of a
+// squaring boundary (squarings_from_estimate); otherwise the lane takes the
+// reference's FP64 norm: column sums over rows as ((x0 + x2) + (x1 + x3))
+// with x_r = |A[r][j]| (+ |G[r][j]|) (csrc/MatrixExpSmall.cuh:144-152), whose
+// total is finite exactly when every entry is (the non-finite rule of
+// :126-140).
+template <bool Pair>
+__device__ __forceinline__ int lane_squarings(const PM<Pair>& a) {
+  uint32_t top = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float c = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      c += __builtin_fabsf(a.d.v[4 * r + j]);
+      if constexpr (Pair) c += __builtin_fabsf(a.u.v[4 * r + j]);
+    }
+    // Bit patterns order non-negative floats, with inf and NaN above all.
+    top = max(top, __float_as_uint(c) & 0x7FFFFFFFu);
+  }
+  int s;
+  if (squarings_from_estimate(__uint_as_float(top), s)) return s;
   double norm = 0.;
   double total = 0.;
 #pragma unroll
@@ -254,95 +398,118 @@ __device__ __forceinline__ void compute_matrix(const ExpmArgs& args, PM<Pair> a,
     norm = fmax(norm, c);
     total += c;
   }
-  const bool bad = !__builtin_isfinite(total);
-  const int s = bad ? 0 : squarings_from_norm(norm);
+  if (!__builtin_isfinite(total)) return -1;
+  return squarings_from_norm(norm);
+}
 
-  // Scale by 2^-s (csrc/MatrixExpSmall.cuh:157-162) with the views' lazy
-  // negation folded into the same exact multiply.
-  const float scale = __builtin_ldexpf(1.f, -s);
-  const float scale_x = scale * args.x.sign;
-  const float scale_g = scale * args.g.sign;
+// Makes the values of m exist at this point of the program, so that their
+// computation is not sunk past later code.
+template <bool Pair>
+__device__ __forceinline__ void pin(PM<Pair>& m) {
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
-    a.d.v[e] *= scale_x;
-    if constexpr (Pair) a.u.v[e] *= scale_g;
+    asm volatile("" : "+v"(m.d.v[e]));
+    if constexpr (Pair) asm volatile("" : "+v"(m.u.v[e]));
   }
+}
 
-  // Degree-18 polynomial (csrc/MatrixExpSmall.cuh:83-106):
-  // A2 = A.A, A3 = A2.A, A6 = A3.A3, A9 = B1.B5 + B4, T = B2 + (B3 + A9).A9.
+// Degree-18 polynomial of this lane's scaled matrix (csrc/MatrixExpSmall.cuh:
+// 83-106): A2 = A.A, A3 = A2.A, A6 = A3.A3, A9 = B1.B5 + B4,
+// T = B2 + (B3 + A9).A9.  Rows of B1..B4 are formed where they are used, and
+// one pass over the rows finishes A9, B3 + A9 and B2 together, so that the
+// powers die row by row and only B5 and the three row outputs are kept whole.
+template <bool Pair>
+__device__ __forceinline__ PM<Pair> t18(const PM<Pair>& a) {
   const PM<Pair> a2 = pmul<Pair>(a, a);
   const PM<Pair> a3 = pmul<Pair>(a2, a);
   const PM<Pair> a6 = pmul<Pair>(a3, a3);
-  PM<Pair> a9;
-  {
-    const PM<Pair> b5 = comb<4, Pair>(a, a2, a3, a6);
+  const PM<Pair> b5 = comb<4, Pair>(a, a2, a3, a6);
+  PM<Pair> a9, lhs, b2;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {  // B1 one row at a time
-      float b1d[4], b1u[4], b4d[4], b4u[4];
-      comb_row<0, Pair>(a, a2, a3, a6, i, b1d, b1u);
-      pmul_row<Pair>(b1d, b1u, b5, &a9.d.v[4 * i], &a9.u.v[4 * i]);
-      comb_row<3, Pair>(a, a2, a3, a6, i, b4d, b4u);
+  for (int i = 0; i < 4; ++i) {
+    float b1d[4], b1u[4], b4d[4], b4u[4];
+    comb_row<0, Pair>(a, a2, a3, a6, i, b1d, b1u);
+    pmul_row<Pair>(b1d, b1u, b5, &a9.d.v[4 * i], &a9.u.v[4 * i]);
+    comb_row<3, Pair>(a, a2, a3, a6, i, b4d, b4u);
+    comb_row<2, Pair>(a, a2, a3, a6, i, &lhs.d.v[4 * i], &lhs.u.v[4 * i]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        a9.d.v[4 * i + j] += b4d[j];
-        if constexpr (Pair) a9.u.v[4 * i + j] += b4u[j];
+    for (int j = 0; j < 4; ++j) {
+      const int e = 4 * i + j;
+      a9.d.v[e] += b4d[j];
+      lhs.d.v[e] += a9.d.v[e];
+      if constexpr (Pair) {
+        a9.u.v[e] += b4u[j];
+        lhs.u.v[e] += a9.u.v[e];
       }
     }
+    comb_row<1, Pair>(a, a2, a3, a6, i, &b2.d.v[4 * i], &b2.u.v[4 * i]);
   }
   PM<Pair> res;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {  // (B3 + A9) and B2 one row at a time
-    float ld[4], lu[4], b2d[4], b2u[4], qd[4], qu[4];
-    comb_row<2, Pair>(a, a2, a3, a6, i, ld, lu);
+  for (int i = 0; i < 4; ++i) {
+    float qd[4], qu[4];
+    pmul_row<Pair>(&lhs.d.v[4 * i], &lhs.u.v[4 * i], a9, qd, qu);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      ld[j] += a9.d.v[4 * i + j];
-      if constexpr (Pair) lu[j] += a9.u.v[4 * i + j];
-    }
-    pmul_row<Pair>(ld, lu, a9, qd, qu);
-    comb_row<1, Pair>(a, a2, a3, a6, i, b2d, b2u);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      res.d.v[4 * i + j] = b2d[j] + qd[j];
-      if constexpr (Pair) res.u.v[4 * i + j] = b2u[j] + qu[j];
+      res.d.v[4 * i + j] = b2.d.v[4 * i + j] + qd[j];
+      if constexpr (Pair) res.u.v[4 * i + j] = b2.u.v[4 * i + j] + qu[j];
     }
   }
-
-  // s squarings per matrix (csrc/MatrixExpSmall.cuh:168); the wavefront loops
-  // while any of its matrices still needs one and each keeps its own result.
-  for (int it = 0; __builtin_amdgcn_ballot_w64(it < s) != 0; ++it) {
-    const PM<Pair> sq = pmul<Pair>(res, res);
-    const bool keep = it < s;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      res.d.v[e] = keep ? sq.d.v[e] : res.d.v[e];
-      if constexpr (Pair) res.u.v[e] = keep ? sq.u.v[e] : res.u.v[e];
-    }
-  }
-
-  M4 outm = Pair ? res.u : res.d;
-  if (bad) {
-#pragma unroll
-    for (int e = 0; e < 16; ++e) outm.v[e] = __builtin_nanf("");
-  }
-  if constexpr (XL != kVecNone) {
-    if (full_group) {
-      store_group_staged<T>(args.out, b - lane, lane, outm, tile);
-    } else if (valid) {
-      store_matrix<T, true>(args.out, b, n, outm);
-    }
-  } else {
-    if (valid) store_matrix<T, false>(args.out, b, n, outm);
-  }
-  if (valid && args.s_out) args.s_out[b] = bad ? -1 : s;
+  return res;
 }
 
-// Persistent kernel: each wavefront walks 64-matrix groups with a grid stride
-// and issues the loads of its next group before computing the current one, so
-// HBM latency overlaps the arithmetic of the previous group.
+// One group's operands between their loads and their turn: raw bytes for the
+// vector classes (dense groups still in the loaded chunk order), converted
+// matrices for element-wise loads.
 template <typename T, bool Pair, int XL, int GL>
-__global__ __launch_bounds__(64 * kP4Waves) void expm_p4_kernel(ExpmArgs args) {
-  __shared__ float stage[kP4Waves][64 * kStageStride];
+struct Staged {
+  static constexpr bool kRaw = XL != kVecNone;
+  RawMat<T> x, g;
+  PM<Pair> m;
+  bool dense_x, dense_g;
+};
+
+template <typename T, bool Pair, int XL, int GL>
+__device__ __forceinline__ void load_group(Staged<T, Pair, XL, GL>& st, const ExpmArgs& args, int64_t group, int lane,
+                                           int n) {
+  const int64_t b = group * 64 + lane;
+  const bool valid = b < args.batch;
+  if constexpr (Staged<T, Pair, XL, GL>::kRaw) {
+    const bool full = (group + 1) * 64 <= args.batch;
+    st.dense_x = full && args.x.dense;
+    st.x = st.dense_x ? load_dense_raw<T>(args.x, group, lane) : load_lane_raw<T, XL>(args.x, b, valid);
+    if constexpr (Pair) {
+      st.dense_g = full && args.g.dense;
+      st.g = st.dense_g ? load_dense_raw<T>(args.g, group, lane) : load_lane_raw<T, GL>(args.g, b, valid);
+    }
+  } else {
+    st.m.d = load_matrix<T, XL>(args.x, b, n, valid);
+    if constexpr (Pair) st.m.u = load_matrix<T, GL>(args.g, b, n, valid);
+  }
+}
+
+template <typename T, bool Pair, int XL, int GL>
+__device__ __forceinline__ PM<Pair> unstage(Staged<T, Pair, XL, GL>& st, float* tile, int lane) {
+  if constexpr (Staged<T, Pair, XL, GL>::kRaw) {
+    if (st.dense_x) dense_to_lane<T>(st.x, tile, lane);
+    PM<Pair> m;
+    m.d = decode<T, XL>(st.x);
+    if constexpr (Pair) {
+      if (st.dense_g) dense_to_lane<T>(st.g, tile + kDenseRowBytes, lane);
+      m.u = decode<T, GL>(st.g);
+    }
+    return m;
+  } else {
+    return st.m;
+  }
+}
+
+// Persistent kernel: each wavefront walks 64-matrix groups with a grid
+// stride and keeps the next group's loads in flight while it computes.
+template <typename T, bool Pair, int XL, int GL>
+__global__ __launch_bounds__(64 * kP4Waves) __attribute__((amdgpu_waves_per_eu(Pair ? 2 : 4, 8))) void expm_p4_kernel(
+    ExpmArgs args) {
+  __shared__ float tile[kP4Waves][kTileFloats<Pair>];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int n = (XL != kVecNone) ? 4 : args.n;
@@ -350,22 +517,64 @@ __global__ __launch_bounds__(64 * kP4Waves) void expm_p4_kernel(ExpmArgs args) {
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kP4Waves;
   int64_t group = static_cast<int64_t>(blockIdx.x) * kP4Waves + wave;
 
-  PM<Pair> next;
-  if (group < groups) {
-    const int64_t b = group * 64 + lane;
-    next.d = load_matrix<T, XL>(args.x, b, n, b < args.batch);
-    if constexpr (Pair) next.u = load_matrix<T, GL>(args.g, b, n, b < args.batch);
-  }
+  Staged<T, Pair, XL, GL> next;
+  if (group < groups) load_group<T, Pair, XL, GL>(next, args, group, lane, n);
   for (; group < groups; group += stride) {
-    const PM<Pair> cur = next;
     const int64_t b = group * 64 + lane;
-    if (group + stride < groups) {
-      const int64_t nb = (group + stride) * 64 + lane;
-      next.d = load_matrix<T, XL>(args.x, nb, n, nb < args.batch);
-      if constexpr (Pair) next.u = load_matrix<T, GL>(args.g, nb, n, nb < args.batch);
+    const bool valid = b < args.batch;
+    PM<Pair> cur = unstage<T, Pair, XL, GL>(next, tile[wave], lane);
+    const int s = lane_squarings<Pair>(cur);
+    const bool bad = s < 0;
+
+    // Scale by 2^-s (csrc/MatrixExpSmall.cuh:157-162) with the views' lazy
+    // negation folded into the same exact multiply.
+    const float scale = __builtin_ldexpf(1.f, bad ? 0 : -s);
+    const float scale_x = scale * args.x.sign;
+    const float scale_g = scale * args.g.sign;
+    PM<Pair> a;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      a.d.v[e] = cur.d.v[e] * scale_x;
+      if constexpr (Pair) a.u.v[e] = cur.u.v[e] * scale_g;
     }
-    const bool full_group = (group + 1) * 64 <= args.batch;
-    compute_matrix<T, Pair, XL>(args, cur, b, n, b < args.batch, lane, full_group, stage[wave]);
+
+    // Next group's loads: before the polynomial in the forward kernel, which
+    // has registers to spare; after it in the Frechet kernel, where the
+    // polynomial sets the register peak.  The staged bytes must not stay live
+    // past this point, so the last group clears them instead of keeping them.
+    auto prefetch = [&]() {
+      if (group + stride < groups) {
+        load_group<T, Pair, XL, GL>(next, args, group + stride, lane, n);
+      } else {
+        next = Staged<T, Pair, XL, GL>{};
+      }
+    };
+    if constexpr (!Pair) prefetch();
+    PM<Pair> res = t18<Pair>(a);
+    pin<Pair>(res);
+    if constexpr (Pair) prefetch();
+
+    // s squarings per matrix (csrc/MatrixExpSmall.cuh:168); the wavefront
+    // loops while any of its matrices still needs one, the others masked off.
+    for (int it = 0; __builtin_amdgcn_ballot_w64(it < s) != 0; ++it) {
+      if (it < s) res = pmul<Pair>(res, res);
+    }
+
+    M4 outm = Pair ? res.u : res.d;
+    if (bad) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) outm.v[e] = __builtin_nanf("");
+    }
+    if constexpr (XL != kVecNone) {
+      if ((group + 1) * 64 <= args.batch) {
+        store_group_staged<T>(args.out, b - lane, lane, outm, tile[wave]);
+      } else if (valid) {
+        store_matrix<T, true>(args.out, b, n, outm);
+      }
+    } else {
+      if (valid) store_matrix<T, false>(args.out, b, n, outm);
+    }
+    if (valid && args.s_out) args.s_out[b] = s;
   }
 }
 

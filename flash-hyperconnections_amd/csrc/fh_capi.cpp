@@ -37,6 +37,7 @@ fh::Operand make_operand(const void* data, const int64_t strides[3], int neg, in
   op.sc = strides[2];
   op.sign = neg ? -1.f : 1.f;
   op.vec = fh::kVecNone;
+  op.dense = 0;
   if (n == 4) {
     // A whole row (or column) of the 4 x 4 matrix is one aligned vector when
     // its elements are adjacent and every matrix/row (column) start keeps the
@@ -45,8 +46,10 @@ fh::Operand make_operand(const void* data, const int64_t strides[3], int neg, in
     const bool base_ok = aligned(data, vbytes) && strides[0] % 4 == 0;
     if (base_ok && strides[2] == 1 && strides[1] % 4 == 0) {
       op.vec = fh::kVecRows;
+      op.dense = strides[0] == 16 && strides[1] == 4 && aligned(data, 16);
     } else if (base_ok && strides[1] == 1 && strides[2] % 4 == 0) {
       op.vec = fh::kVecCols;
+      op.dense = strides[0] == 16 && strides[2] == 4 && aligned(data, 16);
     }
   }
   return op;

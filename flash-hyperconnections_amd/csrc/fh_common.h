@@ -49,6 +49,9 @@ struct F16 {
 // `vec` tells the P == 4 kernel that every row (kVecRows: sc == 1) or every
 // column (kVecCols: sr == 1) of a 4 x 4 matrix is one aligned 4-element
 // vector; the host sets it only when n == 4 and the alignment holds.
+// `dense` adds that the matrices themselves are packed (16 elements apart,
+// rows or columns 4 apart), so 64 consecutive matrices are one contiguous,
+// 16-byte aligned block.
 constexpr int kVecNone = 0;
 constexpr int kVecRows = 1;
 constexpr int kVecCols = 2;
@@ -57,6 +60,7 @@ struct Operand {
   int64_t sb, sr, sc;
   float sign;
   int vec;
+  int dense;
 };
 
 struct ExpmArgs {
@@ -136,7 +140,7 @@ __device__ __forceinline__ int squarings_from_norm(double norm) {
 
 // s from an FP32 estimate of the norm whose relative error is below 2^-18.
 // s(norm) is monotone and steps only where norm / theta18 crosses a power of
-// two, so when the estimate keeps q = norm / theta18 at least 2^-15 (relative)
+// two, so when the estimate keeps q = norm / theta18 at least 2^-16 (relative)
 // away from every power of two, the exact FP64 norm lies on the same step and
 // has the same s.  Returns false -- only the exact norm can decide -- inside
 // those bands and for huge or non-finite estimates.

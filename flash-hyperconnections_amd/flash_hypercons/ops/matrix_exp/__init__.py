@@ -93,20 +93,44 @@ def _expm_debug_fake(input, direction, variant):
     return _matrix_exp_fake(input), input.new_empty((input.shape[0],), dtype=torch.int32)
 
 
+def _frechet_differentiable(input: torch.Tensor, direction: torch.Tensor) -> torch.Tensor:
+    """Differentiable L(input, direction) for a backward that builds a graph.
+
+    The same 2N x 2N block exponential as ``_frechet_reference``, but taken with
+    this build's own operator whenever the block is itself eligible (2N <= 32):
+    its gradient is then again the HIP Frechet kernel, so second derivatives
+    stay on the device.  Larger blocks use the reference's native path.
+    """
+    n = input.shape[-1]
+    if 2 * n > 32 or not _eligible(input):
+        return _frechet_reference(input, direction)
+    a, g = input.float(), direction.float()
+    zero = torch.zeros_like(a)
+    block = torch.cat((torch.cat((a, g), -1), torch.cat((zero, a), -1)), -2)
+    return torch.ops.flash_hypercons._matrix_exp(block)[..., :n, n:].to(input.dtype)
+
+
 def _setup_context(ctx, inputs, output):
     ctx.save_for_backward(inputs[0])
 
 
 def _backward(ctx, grad_output):
-    """Reference :65-74: the gradient of exp at A against G is L(A^T, G)."""
+    """Reference :65-74: the gradient of exp at A against G is L(A^T, G).
+
+    Tensor subclasses, modes and forward-mode tangents take the reference's
+    native block exponential as in the reference; a backward that builds a
+    graph (``create_graph=True``) takes the block exponential through this
+    operator (``_frechet_differentiable``) instead of the native one.
+    """
     (input,) = ctx.saved_tensors
     if (
-        torch.is_grad_enabled()
-        or has_torch_function((input, grad_output))
+        has_torch_function((input, grad_output))
         or torch.autograd.forward_ad.unpack_dual(input).tangent is not None
         or torch.autograd.forward_ad.unpack_dual(grad_output).tangent is not None
     ):
         return _frechet_reference(input.mT, grad_output)
+    if torch.is_grad_enabled():
+        return _frechet_differentiable(input.mT, grad_output)
     return torch.ops.flash_hypercons._frechet(input.mT, grad_output)
 
 

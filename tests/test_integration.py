@@ -46,6 +46,33 @@ def test_double_backward_and_forward_ad(dtype, n):
             check_error(tangent, reference(a, g), backward=True)
 
 
+@pytest.mark.parametrize("n", [2, 4, 8, 9, 16, 17])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_double_backward_stays_on_device(dtype, n):
+    """create_graph=True: the first-order gradient is the top-right block of this operator on
+    [[A^T, G], [0, A^T]] (2N <= 32), so the second derivative runs the Frechet kernel again;
+    beyond 2N = 32 the native block exponential is used as in the reference."""
+    a = (torch.randn(3, n, n, device="cuda") * 0.5).to(dtype).requires_grad_()
+    g, h = torch.randn_like(a), torch.randn_like(a)
+
+    def second_order():
+        (first,) = torch.autograd.grad(fh.matrix_exp(a), a, g, create_graph=True)
+        (second,) = torch.autograd.grad(first, a, h)
+        return first, second
+
+    (first, second), names = op_names(second_order)
+    ref_a = a.detach().double().requires_grad_()
+    (ref_first,) = torch.autograd.grad(reference(ref_a), ref_a, g.double(), create_graph=True)
+    (ref_second,) = torch.autograd.grad(ref_first, ref_a, h.double())
+    check_error(first, ref_first, backward=True)
+    check_error(second, ref_second, backward=True)
+    if 2 * n <= 32:
+        assert "flash_hypercons::_frechet" in names
+        assert "aten::linalg_matrix_exp" not in names
+    else:
+        assert "aten::linalg_matrix_exp" in names
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_function_transforms_use_native(dtype):
     a = (torch.randn(2, 4, 4, device="cuda") * 0.03).to(dtype)

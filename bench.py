@@ -65,6 +65,13 @@ def make_inputs(name: str, torch, device):
         x = base
         g = torch.randn(b, n, n)
         dtype, layout = torch.float32, "transposed view"
+    elif name == "p8":
+        # Not a BASELINE config: the P = 8 kernel (n = 5..8) at [262144, 8, 8] FP32, same
+        # per-matrix scale law as config 5.
+        b, n = 1 << 18, 8
+        x = torch.randn(b, n, n) / n**0.5 * (10 ** torch.empty(b).uniform_(-1, 1))[:, None, None]
+        g = torch.randn(b, n, n)
+        dtype, layout = torch.float32, "contiguous"
     elif name in ("c5", "c5f32"):
         b, n = 32768, 32
         x = torch.randn(b, n, n) / n**0.5 * (10 ** torch.empty(b).uniform_(-1, 1.5))[:, None, None]
@@ -142,10 +149,14 @@ def measure_config(name: str, torch, fh, steps: int, warmup: int, device) -> dic
     bytes_bwd = b * n * n * 3 * e
     flops_fwd = float(((5 + s_f) * 2 * n**3).sum())
     flops_bwd = float(((5 + s_b) * 3 * 2 * n**3).sum())
-    t_hbm = (bytes_fwd + bytes_bwd) / (HBM_PEAK_GBS * 1e9)
-    t_mfma = (flops_fwd + flops_bwd) / (MFMA_F32_PEAK_TFLOPS * 1e12)
-    bound = "hbm" if n <= 8 else "mfma"
-    t_ideal = t_hbm if bound == "hbm" else t_mfma
+    # Roofline time = max(bytes / HBM peak, flops / FP32 matrix peak), per kernel and per step.
+    def ideal(nbytes, nflops):
+        t_hbm, t_mfma = nbytes / (HBM_PEAK_GBS * 1e9), nflops / (MFMA_F32_PEAK_TFLOPS * 1e12)
+        return ("hbm", t_hbm) if t_hbm >= t_mfma else ("mfma", t_mfma)
+
+    bound, t_ideal = ideal(bytes_fwd + bytes_bwd, flops_fwd + flops_bwd)
+    bound_fwd, t_fwd = ideal(bytes_fwd, flops_fwd)
+    bound_bwd, t_bwd = ideal(bytes_bwd, flops_bwd)
     out = {
         "shape": [b, n, n],
         "dtype": str(x.dtype).replace("torch.", ""),
@@ -160,22 +171,20 @@ def measure_config(name: str, torch, fh, steps: int, warmup: int, device) -> dic
         "bound": bound,
         "roofline_frac_step": t_ideal / (ms_step * 1e-3),
         "fwd_kernel": {
+            "bound": bound_fwd,
             "achieved_gbs": bytes_fwd / (ms_fwd * 1e-3) / 1e9,
             "achieved_tflops": flops_fwd / (ms_fwd * 1e-3) / 1e12,
+            "frac": t_fwd / (ms_fwd * 1e-3),
         },
         "bwd_kernel": {
+            "bound": bound_bwd,
             "achieved_gbs": bytes_bwd / (ms_bwd * 1e-3) / 1e9,
             "achieved_tflops": flops_bwd / (ms_bwd * 1e-3) / 1e12,
+            "frac": t_bwd / (ms_bwd * 1e-3),
         },
         "input_sha256": sha256(x)[:16],
         "grad_sha256": sha256(g)[:16],
     }
-    if bound == "hbm":
-        out["fwd_kernel"]["frac"] = out["fwd_kernel"]["achieved_gbs"] / HBM_PEAK_GBS
-        out["bwd_kernel"]["frac"] = out["bwd_kernel"]["achieved_gbs"] / HBM_PEAK_GBS
-    else:
-        out["fwd_kernel"]["frac"] = out["fwd_kernel"]["achieved_tflops"] / MFMA_F32_PEAK_TFLOPS
-        out["bwd_kernel"]["frac"] = out["bwd_kernel"]["achieved_tflops"] / MFMA_F32_PEAK_TFLOPS
     del xin, x, g, xt
     return out
 
@@ -255,7 +264,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baselines")
-    ap.add_argument("--only", default=None, help="comma list of configs (c2,c3,c4,c5,c5f32)")
+    ap.add_argument("--only", default=None, help="comma list of configs (c2,c3,c4,c5,c5f32,p8)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one device copy of exactly 64 MiB (profiler counter calibration)")
     args = ap.parse_args()
@@ -280,7 +289,7 @@ def main() -> int:
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    configs = (args.only or "c2,c3,c4,c5,c5f32").split(",")
+    configs = (args.only or "c2,c3,c4,c5,c5f32,p8").split(",")
     results = {}
     for name in configs:
         log(f"[bench] {name} ...")

@@ -1,10 +1,503 @@
-// P == 8 kernel (n = 5..8).
+// P == 8 kernel (n = 5..8) on the matrix cores: 4 matrices per 64-lane
+// wavefront, every product on v_mfma_f32_4x4x1_16b_f32.
+//
+// Layout: an 8 x 8 matrix is a 2 x 2 arrangement of 4 x 4 blocks spread over
+// one row of 16 lanes: lane l serves matrix slot m = l/16, block (I, J) with
+// I = bit 3 and J = bit 2 of l, and index q = l%4 inside the block.  A
+// matrix value is held in one of two layouts of four VGPRs:
+//   C (columns): v[r] = M[4I + r][4J + q]      R (rows): v[k] = M[4I + q][4J + k].
+// The 4x4x1 MFMA multiplies 16 independent 4 x 4 blocks per instruction
+// (block b's lanes supply A[i][0] from lane 4b+i and B[0][j] from lane 4b+j;
+// D[i][j] lands in lane 4b+j, VGPR i), so output block (I, J) of X.Y is
+//   sum over K = 0, 1 and k = 0..3 of  X_IK[:, k] (x) Y_KJ[k, :].
+// Its A operand is row q of X block (I, K): the lane's own R registers when
+// K == J, else those of the lane 4 positions away; its B operand is column q
+// of Y block (K, J): own C registers when K == I, else those of the lane 8
+// away.  Each K step therefore takes every operand with one bank-masked DPP
+// row rotation (row_ror 4 / 12 for A, row_ror 8 for B; lanes whose block
+// already holds the operand keep their own value), and steps run K = 0, 1 in
+// turn -- the products accumulate k = 0..7 in the reference's order from +0,
+// each step one exact FMA (csrc/MatrixExpSmall.cuh:31-33).  Left operands
+// reach the R layout through an LDS transpose of each block in place.
+//
+// Arithmetic is the reference's, element by element (csrc/MatrixExpSmall.cuh:
+// 22-106): Frechet U blocks sum D.U and U.D separately and add them, combines
+// are the contracted chain with zero coefficients skipped, the FP64 norm uses
+// the P = 8 butterfly.  Results are bit-identical to that evaluation up to the
+// sign of zero results.
 #include "fh_kernels.h"
 
 namespace fh {
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kOctWaves = 4;     // wavefronts per workgroup
+constexpr int kOctUnit = 4;      // matrices per wavefront
+constexpr int kOctLds = 512;     // floats per wavefront: two 4 x 64 transpose planes
+
+constexpr int kRor4 = 0x124;     // DPP row_ror:4  (lane l reads lane l - 4 of its row of 16)
+constexpr int kRor8 = 0x128;     // DPP row_ror:8
+constexpr int kRor12 = 0x12C;    // DPP row_ror:12 (lane l reads lane l + 4)
+
+struct Q {
+  float v[4];
+};
+
+template <bool Pair>
+struct PQ {
+  Q d;
+  Q u;
+};
+
+// Compiler ordering of the wavefront's LDS accesses (the hardware performs
+// one wavefront's LDS operations in issue order).
+__device__ __forceinline__ void lds_order() {
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+}
+
+// Transpose of every 4 x 4 block in place (C <-> R) through the wavefront's
+// LDS plane t (256 floats): lane (b, q), b = lane/4, writes its four values
+// as one 16-byte chunk to plane row q, slot b ^ 2q, and reads back element q
+// of slot b from the four plane rows (XOR swizzle: no bank conflicts).
+__device__ __forceinline__ void plane_write(const Q& m, float* t, int lane) {
+  const int b = lane >> 2, q = lane & 3;
+  *reinterpret_cast<float4*>(t + q * 64 + 4 * (b ^ (2 * q))) = make_float4(m.v[0], m.v[1], m.v[2], m.v[3]);
+}
+__device__ __forceinline__ Q plane_read(const float* t, int lane) {
+  const int b = lane >> 2, q = lane & 3;
+  Q r;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) r.v[k] = t[k * 64 + 4 * (b ^ (2 * k)) + q];
+  return r;
+}
+
+template <bool Pair>
+__device__ __forceinline__ PQ<Pair> ptranspose(const PQ<Pair>& a, float* t, int lane) {
+  plane_write(a.d, t, lane);
+  if constexpr (Pair) plane_write(a.u, t + 256, lane);
+  lds_order();
+  PQ<Pair> r;
+  r.d = plane_read(t, lane);
+  if constexpr (Pair) r.u = plane_read(t + 256, lane);
+  lds_order();
+  return r;
+}
+
+// Lanes in the banks (groups of 4 lanes of a row of 16) set in `Banks` take
+// the value rotated in by `Ctrl`; the others keep their own.
+template <int Ctrl, int Banks>
+__device__ __forceinline__ float dpp_take(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), Ctrl, 0xF, Banks, false));
+}
+
+// A operands of block step K from the R layout of X: banks with J != K
+// (J is bit 0 of the bank) take the lane 4 away.
+template <int K>
+__device__ __forceinline__ Q a_operand(const Q& xr) {
+  Q r;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) r.v[k] = K == 0 ? dpp_take<kRor4, 0xA>(xr.v[k]) : dpp_take<kRor12, 0x5>(xr.v[k]);
+  return r;
+}
+// B operands of block step K from the C layout of Y: banks with I != K (I is
+// bit 1 of the bank) take the lane 8 away.
+template <int K>
+__device__ __forceinline__ Q b_operand(const Q& yc) {
+  Q r;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) r.v[k] = K == 0 ? dpp_take<kRor8, 0xC>(yc.v[k]) : dpp_take<kRor8, 0x3>(yc.v[k]);
+  return r;
+}
+
+// One block product chain: k = 0..7 (K = 0 block first), from +0.
+__device__ __forceinline__ Q chain(const Q& a0, const Q& b0, const Q& a1, const Q& b1) {
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a0.v[k], b0.v[k], acc, 0, 0, 0);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a1.v[k], b1.v[k], acc, 0, 0, 0);
+  return Q{{acc[0], acc[1], acc[2], acc[3]}};
+}
+
+// Structured (Frechet) product (D1.D2, D1.U2 + U1.D2) in C layout from X in
+// R layout and Y in C layout; the two U sums are kept separate and added last
+// (csrc/MatrixExpSmall.cuh:34-49).
+template <bool Pair>
+__device__ __forceinline__ PQ<Pair> pmm(const PQ<Pair>& xr, const PQ<Pair>& yc) {
+  const Q ad0 = a_operand<0>(xr.d), ad1 = a_operand<1>(xr.d);
+  const Q bd0 = b_operand<0>(yc.d), bd1 = b_operand<1>(yc.d);
+  PQ<Pair> c;
+  c.d = chain(ad0, bd0, ad1, bd1);
+  if constexpr (Pair) {
+    const Q u = chain(ad0, b_operand<0>(yc.u), ad1, b_operand<1>(yc.u));
+    const Q v = chain(a_operand<0>(xr.u), bd0, a_operand<1>(xr.u), bd1);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) c.u.v[r] = u.v[r] + v.v[r];
+  }
+  return c;
+}
+
+// B(K+1) = c0*I + c1*A + c2*A^2 + c3*A^3 + c6*A^6 in C layout, the contracted
+// chain of csrc/MatrixExpSmall.cuh:74-77 with zero coefficients skipped;
+// `diag` is 1 in the VGPR holding a diagonal entry and 0 elsewhere.  U blocks
+// have no identity term and start from c1*A.
+template <int K, bool Pair>
+__device__ __forceinline__ PQ<Pair> comb(const PQ<Pair>& a, const PQ<Pair>& a2, const PQ<Pair>& a3,
+                                         const PQ<Pair>& a6, const Q& diag) {
+  constexpr float c0 = kCoef[K][0], c1 = kCoef[K][1], c2 = kCoef[K][2], c3 = kCoef[K][3], c6 = kCoef[K][4];
+  PQ<Pair> b;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float t;
+    if constexpr (c1 != 0.f) {
+      t = __builtin_fmaf(c1, a.d.v[r], c0 * diag.v[r]);
+    } else {
+      t = c0 * diag.v[r];
+    }
+    t = __builtin_fmaf(c2, a2.d.v[r], t);
+    t = __builtin_fmaf(c3, a3.d.v[r], t);
+    if constexpr (c6 != 0.f) t = __builtin_fmaf(c6, a6.d.v[r], t);
+    b.d.v[r] = t;
+    if constexpr (Pair) {
+      float w;
+      if constexpr (c1 != 0.f) {
+        w = c1 * a.u.v[r];
+        w = __builtin_fmaf(c2, a2.u.v[r], w);
+      } else {
+        w = c2 * a2.u.v[r];
+      }
+      w = __builtin_fmaf(c3, a3.u.v[r], w);
+      if constexpr (c6 != 0.f) w = __builtin_fmaf(c6, a6.u.v[r], w);
+      b.u.v[r] = w;
+    }
+  }
+  return b;
+}
+
+template <bool Pair>
+__device__ __forceinline__ PQ<Pair> padd(const PQ<Pair>& a, const PQ<Pair>& b) {
+  PQ<Pair> c;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    c.d.v[r] = a.d.v[r] + b.d.v[r];
+    if constexpr (Pair) c.u.v[r] = a.u.v[r] + b.u.v[r];
+  }
+  return c;
+}
+
+// Degree-18 polynomial of the scaled pair in both layouts
+// (csrc/MatrixExpSmall.cuh:83-106): A2 = A.A, A3 = A2.A, A6 = A3.A3,
+// A9 = B1.B5 + B4, T = B2 + (B3 + A9).A9.  Result in C layout.
+template <bool Pair>
+__device__ __forceinline__ PQ<Pair> t18(const PQ<Pair>& ar, const PQ<Pair>& ac, const Q& diag, float* t,
+                                        int lane) {
+  const PQ<Pair> a2 = pmm<Pair>(ar, ac);
+  const PQ<Pair> a3 = pmm<Pair>(ptranspose<Pair>(a2, t, lane), ac);
+  const PQ<Pair> a6 = pmm<Pair>(ptranspose<Pair>(a3, t, lane), a3);
+  const PQ<Pair> b1r = ptranspose<Pair>(comb<0, Pair>(ac, a2, a3, a6, diag), t, lane);
+  PQ<Pair> a9 = pmm<Pair>(b1r, comb<4, Pair>(ac, a2, a3, a6, diag));
+  a9 = padd<Pair>(a9, comb<3, Pair>(ac, a2, a3, a6, diag));
+  const PQ<Pair> lhsr = ptranspose<Pair>(padd<Pair>(comb<2, Pair>(ac, a2, a3, a6, diag), a9), t, lane);
+  return padd<Pair>(comb<1, Pair>(ac, a2, a3, a6, diag), pmm<Pair>(lhsr, a9));
+}
+
+// ---- norm ---------------------------------------------------------------------
+
+// Exchange with the lane whose bank index differs in bit 0 (lane ^ 4) or bit 1
+// (lane ^ 8) within the row of 16.
+__device__ __forceinline__ int xor4_i(int v) {
+  const int t = __builtin_amdgcn_update_dpp(v, v, kRor4, 0xF, 0xA, false);
+  return __builtin_amdgcn_update_dpp(t, v, kRor12, 0xF, 0x5, false);
+}
+__device__ __forceinline__ int xor8_i(int v) { return __builtin_amdgcn_update_dpp(v, v, kRor8, 0xF, 0xF, false); }
+__device__ __forceinline__ double xor8_d(double v) {
+  const int2 w = __builtin_bit_cast(int2, v);
+  return __builtin_bit_cast(double, make_int2(xor8_i(w.x), xor8_i(w.y)));
+}
+template <int Ctrl>
+__device__ __forceinline__ double dpp_d(double v) {
+  const int2 w = __builtin_bit_cast(int2, v);
+  return __builtin_bit_cast(double, make_int2(__builtin_amdgcn_update_dpp(w.x, w.x, Ctrl, 0xF, 0xF, false),
+                                              __builtin_amdgcn_update_dpp(w.y, w.y, Ctrl, 0xF, 0xF, false)));
+}
+__device__ __forceinline__ double xor4_d(double v) {
+  const int2 w = __builtin_bit_cast(int2, v);
+  return __builtin_bit_cast(double, make_int2(xor4_i(w.x), xor4_i(w.y)));
+}
+
+// Maximum of a non-negative float's bit pattern over the 8 columns of the
+// lane's matrix (lanes differing in bits 0, 1 and the bank's J bit).
+__device__ __forceinline__ uint32_t matrix_max_u32(uint32_t v) {
+  v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), 0xB1, 0xF, 0xF, false)));
+  v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), 0x4E, 0xF, 0xF, false)));
+  return max(v, static_cast<uint32_t>(xor4_i(static_cast<int>(v))));
+}
+
+// Squaring count of the lane's matrix, or -1 for a non-finite one.  The FP32
+// estimate of the column-sum norm decides s unless it lies near a squaring
+// boundary (squarings_from_estimate); then the matrix takes the reference's
+// FP64 norm: per column the butterfly ((x0 + x4) + (x2 + x6)) +
+// ((x1 + x5) + (x3 + x7)) with x_r = |A[r][j]| (+ |G[r][j]|)
+// (csrc/MatrixExpSmall.cuh:144-152), whose total is finite exactly when every
+// entry is (:126-140).  The lanes of blocks (0, J) and (1, J) hold rows 0-3
+// and 4-7 of the same columns.
+template <bool Pair>
+__device__ __forceinline__ int matrix_squarings(const PQ<Pair>& ac, int I) {
+  float p = 0.f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    p += __builtin_fabsf(ac.d.v[r]);
+    if constexpr (Pair) p += __builtin_fabsf(ac.u.v[r]);
+  }
+  p += __int_as_float(xor8_i(__float_as_int(p)));
+  const uint32_t top = matrix_max_u32(__float_as_uint(p) & 0x7FFFFFFFu);
+  int s;
+  const bool decided = squarings_from_estimate(__uint_as_float(top), s);
+  if (__builtin_amdgcn_ballot_w64(!decided) == 0) return s;
+  // Some matrix needs the exact norm: the whole wavefront computes it (the DPP
+  // exchanges need every lane) and the decided matrices keep their estimate.
+  double own[4], other[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    own[r] = fabs(static_cast<double>(ac.d.v[r]));
+    if constexpr (Pair) own[r] += fabs(static_cast<double>(ac.u.v[r]));
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) other[r] = xor8_d(own[r]);
+  double x[8];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    x[r] = I == 0 ? own[r] : other[r];
+    x[4 + r] = I == 0 ? other[r] : own[r];
+  }
+  double norm = ((x[0] + x[4]) + (x[2] + x[6])) + ((x[1] + x[5]) + (x[3] + x[7]));
+  double total = norm;
+  norm = fmax(norm, dpp_d<0xB1>(norm));
+  total = total + dpp_d<0xB1>(total);
+  norm = fmax(norm, dpp_d<0x4E>(norm));
+  total = total + dpp_d<0x4E>(total);
+  norm = fmax(norm, xor4_d(norm));
+  total = total + xor4_d(total);
+  if (decided) return s;
+  if (!__builtin_isfinite(total)) return -1;
+  return squarings_from_norm(norm);
+}
+
+// ---- loads / stores -------------------------------------------------------------
+//
+// Layout classes (set by the host for n == 8): kVecRows -- every row of a
+// matrix is made of aligned 4-element vectors (sc == 1), loaded straight into
+// the R layout; kVecCols -- every column is (sr == 1), loaded into the C
+// layout; kVecNone -- element loads through the strides into the C layout,
+// zero padded for n < 8.  Raw storage bits are kept until the unit's turn.
+
+template <typename T>
+struct Raw4 {
+  typename T::storage v[4];
+};
+
+template <typename T, int L>
+__device__ __forceinline__ Raw4<T> load_raw(const Operand& op, int64_t m, int I, int J, int q, int n, bool valid) {
+  using S = typename T::storage;
+  Raw4<T> w;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) w.v[r] = S{};
+  if (!valid) return w;
+  const S* base = static_cast<const S*>(op.data) + m * op.sb;
+  if constexpr (L == kVecRows) {
+    typedef S S4 __attribute__((ext_vector_type(4)));
+    const S4 x = *reinterpret_cast<const S4*>(base + (4 * I + q) * op.sr + 4 * J);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) w.v[r] = x[r];
+  } else if constexpr (L == kVecCols) {
+    typedef S S4 __attribute__((ext_vector_type(4)));
+    const S4 x = *reinterpret_cast<const S4*>(base + (4 * J + q) * op.sc + 4 * I);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) w.v[r] = x[r];
+  } else {
+    const int col = 4 * J + q;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 4 * I + r;
+      if (row < n && col < n) w.v[r] = base[row * op.sr + col * op.sc];
+    }
+  }
+  return w;
+}
+
+template <typename T>
+__device__ __forceinline__ Q to_q(const Raw4<T>& w) {
+  Q m;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) m.v[r] = to_f32<T>(w.v[r]);
+  return m;
+}
+
+template <typename T, bool Pair, int XL, int GL>
+struct UnitRaw {
+  Raw4<T> x;
+  Raw4<T> g;
+};
+
+// ---- kernel -----------------------------------------------------------------
+
+// Persistent kernel: each wavefront walks 4-matrix units with a grid stride
+// and issues the next unit's loads before computing the current one.
+template <typename T, bool Pair, int XL, int GL>
+__global__ __launch_bounds__(64 * kOctWaves) void expm_oct_kernel(ExpmArgs args) {
+  using S = typename T::storage;
+  __shared__ float lds[kOctWaves][kOctLds];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  float* t = lds[wave];
+  const int slot = lane >> 4;
+  const int I = (lane >> 3) & 1;
+  const int J = (lane >> 2) & 1;
+  const int q = lane & 3;
+  const int n = (XL != kVecNone) ? 8 : args.n;
+  Q diag;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) diag.v[r] = (I == J && r == q) ? 1.f : 0.f;
+  const int64_t units = (args.batch + kOctUnit - 1) / kOctUnit;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kOctWaves;
+  int64_t unit = static_cast<int64_t>(blockIdx.x) * kOctWaves + wave;
+
+  auto load_unit = [&](int64_t u) {
+    UnitRaw<T, Pair, XL, GL> r;
+    const int64_t m = u * kOctUnit + slot;
+    const bool valid = m < args.batch;
+    r.x = load_raw<T, XL>(args.x, m, I, J, q, n, valid);
+    if constexpr (Pair) r.g = load_raw<T, GL>(args.g, m, I, J, q, n, valid);
+    return r;
+  };
+
+  UnitRaw<T, Pair, XL, GL> next;
+  if (unit < units) next = load_unit(unit);
+  for (; unit < units; unit += stride) {
+    const int64_t m = unit * kOctUnit + slot;
+    const bool valid = m < args.batch;
+    PQ<Pair> lx;  // as loaded: R layout for kVecRows, C layout otherwise
+    lx.d = to_q<T>(next.x);
+    if constexpr (Pair) lx.u = to_q<T>(next.g);
+    if (unit + stride < units) next = load_unit(unit + stride);
+
+    // Both layouts of X (and G).
+    PQ<Pair> ar, ac;
+    {
+      const PQ<Pair> other = ptranspose<Pair>(lx, t, lane);
+      ar.d = XL == kVecRows ? lx.d : other.d;
+      ac.d = XL == kVecRows ? other.d : lx.d;
+      if constexpr (Pair) {
+        ar.u = GL == kVecRows ? lx.u : other.u;
+        ac.u = GL == kVecRows ? other.u : lx.u;
+      }
+    }
+
+    const int s = matrix_squarings<Pair>(ac, I);
+    const bool bad = s < 0;
+
+    // Scale by 2^-s (csrc/MatrixExpSmall.cuh:157-162) with the views' lazy
+    // negation folded into the same exact multiply.
+    const float scale = __builtin_ldexpf(1.f, bad ? 0 : -s);
+    const float scale_x = scale * args.x.sign;
+    const float scale_g = scale * args.g.sign;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      ar.d.v[r] *= scale_x;
+      ac.d.v[r] *= scale_x;
+      if constexpr (Pair) {
+        ar.u.v[r] *= scale_g;
+        ac.u.v[r] *= scale_g;
+      }
+    }
+
+    PQ<Pair> res = t18<Pair>(ar, ac, diag, t, lane);
+
+    // s squarings per matrix (csrc/MatrixExpSmall.cuh:168); the wavefront
+    // loops while any of its matrices still needs one and each keeps its own
+    // result.
+    for (int it = 0; __builtin_amdgcn_ballot_w64(it < s) != 0; ++it) {
+      const PQ<Pair> sq = pmm<Pair>(ptranspose<Pair>(res, t, lane), res);
+      const bool keep = it < s;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        res.d.v[r] = keep ? sq.d.v[r] : res.d.v[r];
+        if constexpr (Pair) res.u.v[r] = keep ? sq.u.v[r] : res.u.v[r];
+      }
+    }
+
+    Q out = Pair ? res.u : res.d;
+    if (bad) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) out.v[r] = __builtin_nanf("");
+    }
+    if constexpr (XL != kVecNone) {
+      // n == 8: each lane writes 4 consecutive entries of a row from the R layout.
+      plane_write(out, t, lane);
+      lds_order();
+      const Q row = plane_read(t, lane);
+      lds_order();
+      if (valid) {
+        typedef S S4 __attribute__((ext_vector_type(4)));
+        S4 w;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w[k] = from_f32<T>(row.v[k]);
+        *reinterpret_cast<S4*>(static_cast<S*>(args.out) + m * 64 + (4 * I + q) * 8 + 4 * J) = w;
+      }
+    } else if (valid) {
+      S* o = static_cast<S*>(args.out) + m * n * n;
+      const int col = 4 * J + q;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 4 * I + r;
+        if (row < n && col < n) o[row * n + col] = from_f32<T>(out.v[r]);
+      }
+    }
+    if (valid && (lane & 15) == 0 && args.s_out) args.s_out[m] = s;
+  }
+}
+
+template <typename T, bool Pair, int XL, int GL>
+hipError_t launch_oct_l(const ExpmArgs& args, hipStream_t stream) {
+  // Persistent grid: as many workgroups as the device keeps resident at once.
+  static const int64_t resident =
+      resident_blocks(reinterpret_cast<const void*>(&expm_oct_kernel<T, Pair, XL, GL>), 64 * kOctWaves);
+  const int64_t units = (args.batch + kOctUnit - 1) / kOctUnit;
+  int64_t grid = (units + kOctWaves - 1) / kOctWaves;
+  if (grid > resident) grid = resident;
+  hipLaunchKernelGGL((expm_oct_kernel<T, Pair, XL, GL>), dim3(static_cast<unsigned>(grid)), dim3(64 * kOctWaves), 0,
+                     stream, args);
+  return hipGetLastError();
+}
+
+// n < 8 or an unclassified stride pattern takes the element-wise loader; for
+// n == 8 each operand is classified independently (the output is row-major).
+template <typename T, bool Pair>
+hipError_t launch_oct_t(const ExpmArgs& args, hipStream_t stream) {
+  const int xl = args.n == 8 ? args.x.vec : kVecNone;
+  const int gl = (Pair && args.n == 8) ? args.g.vec : kVecNone;
+  if (xl == kVecNone || (Pair && gl == kVecNone)) return launch_oct_l<T, Pair, kVecNone, kVecNone>(args, stream);
+  if constexpr (Pair) {
+    if (xl == kVecRows) {
+      return gl == kVecRows ? launch_oct_l<T, Pair, kVecRows, kVecRows>(args, stream)
+                            : launch_oct_l<T, Pair, kVecRows, kVecCols>(args, stream);
+    }
+    return gl == kVecRows ? launch_oct_l<T, Pair, kVecCols, kVecRows>(args, stream)
+                          : launch_oct_l<T, Pair, kVecCols, kVecCols>(args, stream);
+  } else {
+    return xl == kVecRows ? launch_oct_l<T, Pair, kVecRows, kVecNone>(args, stream)
+                          : launch_oct_l<T, Pair, kVecCols, kVecNone>(args, stream);
+  }
+}
+
+}  // namespace
 
 hipError_t launch_oct(const ExpmArgs& args, int dtype, bool pair, hipStream_t stream) {
-  return launch_generic(args, dtype, 8, pair, stream);
+  if (dtype == F32::code) return pair ? launch_oct_t<F32, true>(args, stream) : launch_oct_t<F32, false>(args, stream);
+  if (dtype == BF16::code) return pair ? launch_oct_t<BF16, true>(args, stream) : launch_oct_t<BF16, false>(args, stream);
+  return pair ? launch_oct_t<F16, true>(args, stream) : launch_oct_t<F16, false>(args, stream);
 }
 
 }  // namespace fh

@@ -38,18 +38,19 @@ fh::Operand make_operand(const void* data, const int64_t strides[3], int neg, in
   op.sign = neg ? -1.f : 1.f;
   op.vec = fh::kVecNone;
   op.dense = 0;
-  if (n == 4) {
-    // A whole row (or column) of the 4 x 4 matrix is one aligned vector when
-    // its elements are adjacent and every matrix/row (column) start keeps the
-    // vector alignment.
+  if (n == 4 || n == 8) {
+    // Every row (or column) of the matrix is made of aligned 4-element
+    // vectors when its elements are adjacent and every matrix/row (column)
+    // start keeps the vector alignment; for n == 4 the 64 matrices of a group
+    // are one contiguous block (`dense`) when they are packed as well.
     const int64_t vbytes = 4 * element_size(dtype);
     const bool base_ok = aligned(data, vbytes) && strides[0] % 4 == 0;
     if (base_ok && strides[2] == 1 && strides[1] % 4 == 0) {
       op.vec = fh::kVecRows;
-      op.dense = strides[0] == 16 && strides[1] == 4 && aligned(data, 16);
+      op.dense = n == 4 && strides[0] == 16 && strides[1] == 4 && aligned(data, 16);
     } else if (base_ok && strides[1] == 1 && strides[2] % 4 == 0) {
       op.vec = fh::kVecCols;
-      op.dense = strides[0] == 16 && strides[2] == 4 && aligned(data, 16);
+      op.dense = n == 4 && strides[0] == 16 && strides[2] == 4 && aligned(data, 16);
     }
   }
   return op;

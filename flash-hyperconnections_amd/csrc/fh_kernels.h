@@ -13,7 +13,7 @@ int64_t resident_blocks(const void* kernel, int block);
 hipError_t launch_generic(const ExpmArgs& args, int dtype, int P, bool pair, hipStream_t stream);
 // P == 4: one matrix per lane, 64 per wavefront, plain FP32 FMAs.
 hipError_t launch_p4(const ExpmArgs& args, int dtype, bool pair, hipStream_t stream);
-// P == 8: 4 matrices per wavefront as 2x2 blocks of 4x4 MFMA tiles.
+// P == 8: 4 matrices per wavefront as 2x2 blocks of 4x4x1 MFMA tiles.
 hipError_t launch_oct(const ExpmArgs& args, int dtype, bool pair, hipStream_t stream);
 // P in {16, 32}: one wavefront per matrix on 16x16x4 / 32x32x2 MFMA.
 hipError_t launch_tile(const ExpmArgs& args, int dtype, int P, bool pair, hipStream_t stream);

@@ -4,8 +4,9 @@
   oracle for every matrix, in both directions, for every size class and dtype.
 * The generic kernel (FH_VARIANT_GENERIC) evaluates in the reference's exact
   order and must match the oracle bit for bit.
-* The tuned P == 4 kernel (one matrix per lane, plain FP32 FMAs) keeps the
-  reference's evaluation order and must also match the oracle bit for bit.
+* The tuned P == 4 kernel (one matrix per lane, plain FP32 FMAs) and the P == 8
+  kernel (2 x 2 blocks of exact 4x4x1 MFMA steps) keep the reference's
+  evaluation order and must also match the oracle bit for bit.
 * Every kernel must meet the FP32 / FP16 / BF16 tolerances against FP64.
 Inputs are seeded; GPU results are compared through the C ABI that the
 ``flash_hypercons::_expm_debug`` / ``_expm_params`` operators wrap.
@@ -92,8 +93,10 @@ def test_tuned_squarings_and_tolerance(n, dtype, backward):
 
 @pytest.mark.parametrize("backward", [False, True])
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("n", [2, 3, 4])
-def test_quad_kernel_bitwise(n, dtype, backward):
+@pytest.mark.parametrize("n", [2, 3, 4, 5, 6, 7, 8])
+def test_small_kernels_bitwise(n, dtype, backward):
+    """The P = 4 (one matrix per lane) and P = 8 (4x4x1 MFMA blocks) kernels keep the
+    reference's evaluation order and match the oracle bit for bit."""
     a, g = scaled_inputs(1000, n, dtype, seed=3000 * n + 7 * backward + DTYPES.index(dtype))
     a, g = a.cuda(), g.cuda()
     x = a.mT if backward else a

@@ -137,23 +137,79 @@ def _backward(ctx, grad_output):
 torch.library.register_autograd("flash_hypercons::_matrix_exp", _backward, setup_context=_setup_context)
 
 
+def _tangent(input: torch.Tensor, tangent: torch.Tensor) -> torch.Tensor:
+    """L(input, tangent), the forward-mode derivative of exp at input along tangent.
+
+    The Frechet kernel without the backward's transpose.  A computation that
+    builds a graph takes the differentiable block exponential
+    (``_frechet_differentiable``); a tangent the operator cannot take (another
+    dtype, device or layout) takes the reference's native block exponential.
+    """
+    if (
+        not isinstance(tangent, torch.Tensor)
+        or type(tangent) is not torch.Tensor
+        or tangent.layout != torch.strided
+        or tangent.shape != input.shape
+        or tangent.dtype != input.dtype
+        or tangent.device != input.device
+        or torch.autograd.forward_ad.unpack_dual(tangent).tangent is not None
+    ):
+        return _frechet_reference(input, tangent)
+    if torch.is_grad_enabled() and (input.requires_grad or tangent.requires_grad):
+        return _frechet_differentiable(input, tangent)
+    return torch.ops.flash_hypercons._frechet(input, tangent)
+
+
+class _DualMatrixExp(torch.autograd.Function):
+    """exp(A) for an input that carries a forward-mode tangent H.
+
+    The reference sends such inputs to the native exponential
+    (ops/matrix_exp/__init__.py:89-94); here the primal runs the forward kernel
+    and the tangent is L(A, H) from the Frechet kernel.  Reverse mode is the
+    operator's own backward (``_backward``), which sees the saved input with its
+    tangent, so forward-over-reverse keeps working through the native block
+    exponential as in the reference.
+    """
+
+    @staticmethod
+    def forward(input):
+        return torch.ops.flash_hypercons._matrix_exp(input)
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        ctx.save_for_backward(inputs[0])
+        ctx.save_for_forward(inputs[0])
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        return _backward(ctx, grad_output)
+
+    @staticmethod
+    def jvp(ctx, tangent):
+        (input,) = ctx.saved_tensors
+        return _tangent(input, tangent)
+
+
 def matrix_exp(input: torch.Tensor) -> torch.Tensor:
     """Compute exp(input), accelerating ROCm [B, N, N] tensors with 2 <= N <= 32 on gfx950.
 
     The HIP implementation accepts float32, float16, and bfloat16. Other
-    inputs use native PyTorch. Forward AD, function transforms, and tensor
-    subclasses also use native operations; their GPU low-precision inputs
-    are promoted to float32 for the calculation and cast back on return.
+    inputs use native PyTorch. An eligible input carrying a forward-mode
+    tangent gets its tangent from the Frechet kernel. Function transforms,
+    tensor subclasses and forward-mode inputs that are not eligible use native
+    operations; their GPU low-precision inputs are promoted to float32 for the
+    calculation and cast back on return.
     """
     # Check transforms before shape eligibility: vmap can hide batch dimensions.
     if isinstance(input, torch.Tensor) and (
-        type(input) not in (torch.Tensor, torch.nn.Parameter)
-        or torch._C._are_functorch_transforms_active()
-        or torch.autograd.forward_ad.unpack_dual(input).tangent is not None
+        type(input) not in (torch.Tensor, torch.nn.Parameter) or torch._C._are_functorch_transforms_active()
     ):
         return _native(input, promote=True)
+    dual = isinstance(input, torch.Tensor) and torch.autograd.forward_ad.unpack_dual(input).tangent is not None
     if not _eligible(input):
-        return _native(input)
+        return _native(input, promote=dual)
+    if dual:
+        return _DualMatrixExp.apply(input)
     return torch.ops.flash_hypercons._matrix_exp(input)
 
 

@@ -8,7 +8,7 @@ import pytest
 import torch
 
 import flash_hypercons as fh
-from tests.reference import check_error, reference
+from tests.reference import check_error, check_north_star, reference
 from tests.test_routing import op_names
 
 pytestmark = pytest.mark.gpu
@@ -41,9 +41,71 @@ def test_double_backward_and_forward_ad(dtype, n):
             dual = torch.autograd.forward_ad.make_dual(a, g)
             output, names = op_names(lambda dual=dual: torch.linalg.matrix_exp(dual))
             primal, tangent = torch.autograd.forward_ad.unpack_dual(output)
-            assert "flash_hypercons::_matrix_exp" not in names
+            # The reference sends forward-mode inputs to the native exponential; here the
+            # primal runs the forward kernel and the tangent the Frechet kernel.
+            assert "flash_hypercons::_matrix_exp" in names
             check_error(primal, reference(a))
             check_error(tangent, reference(a, g), backward=True)
+
+
+@pytest.mark.parametrize("n", [2, 4, 8, 9, 16, 17, 32])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_forward_ad_tangent_from_frechet_kernel(dtype, n):
+    """A dual input: the primal is this operator's forward and the tangent L(A, H) its Frechet
+    kernel (no transpose), both to the north-star tolerances."""
+    a = (torch.randn(5, n, n, device="cuda") * 0.7).to(dtype)
+    h = torch.randn_like(a)
+    with torch.autograd.forward_ad.dual_level():
+        dual = torch.autograd.forward_ad.make_dual(a, h)
+        output, names = op_names(lambda: fh.matrix_exp(dual))
+        primal, tangent = torch.autograd.forward_ad.unpack_dual(output)
+    assert "flash_hypercons::_matrix_exp" in names
+    assert "flash_hypercons::_frechet" in names
+    assert "aten::linalg_matrix_exp" not in names
+    check_north_star(primal, reference(a))
+    check_north_star(tangent, reference(a, h), backward=True)
+    # Bit-identical to the operators called directly.
+    assert torch.equal(primal, torch.ops.flash_hypercons._matrix_exp(a))
+    assert torch.equal(tangent, torch.ops.flash_hypercons._frechet(a, h))
+
+
+@pytest.mark.parametrize("layout", ["transposed", "expanded", "float64"])
+def test_forward_ad_tangent_layouts(layout):
+    """Tangents the operator cannot take as they are (another dtype) use the native block
+    exponential; strided ones (a transposed view, a broadcast with stride 0) go to the kernel."""
+    a = torch.randn(4, 4, 4, device="cuda") * 0.5
+    if layout == "transposed":
+        h = torch.randn(4, 4, 4, device="cuda").mT
+    elif layout == "expanded":
+        h = torch.randn(1, 4, 4, device="cuda").expand(4, 4, 4)
+    else:
+        a = a.double()
+        h = torch.randn(4, 4, 4, device="cuda", dtype=torch.float64)
+    with torch.autograd.forward_ad.dual_level():
+        dual = torch.autograd.forward_ad.make_dual(a, h)
+        output, names = op_names(lambda: fh.matrix_exp(dual))
+        primal, tangent = torch.autograd.forward_ad.unpack_dual(output)
+    if layout == "float64":
+        assert "flash_hypercons::_matrix_exp" not in names  # float64 is not eligible at all
+    else:
+        assert "flash_hypercons::_frechet" in names
+    check_error(primal, reference(a))
+    check_error(tangent, reference(a, h), backward=True)
+
+
+@pytest.mark.parametrize("n", [4, 9, 16])
+def test_reverse_over_forward(n):
+    """The tangent built with grad enabled is differentiable: d/dA <L(A, H), W> matches FP64."""
+    a = (torch.randn(3, n, n, device="cuda") * 0.5).requires_grad_()
+    h, w = torch.randn_like(a), torch.randn_like(a)
+    with torch.autograd.forward_ad.dual_level():
+        dual = torch.autograd.forward_ad.make_dual(a, h)
+        tangent = torch.autograd.forward_ad.unpack_dual(fh.matrix_exp(dual)).tangent
+        (grad,) = torch.autograd.grad(tangent, a, w)
+    ref_a = a.detach().double().requires_grad_()
+    (ref_grad,) = torch.autograd.grad(reference(ref_a, h.double()), ref_a, w.double())
+    check_error(tangent, reference(a.detach(), h), backward=True)
+    check_error(grad, ref_grad, backward=True)
 
 
 @pytest.mark.parametrize("n", [2, 4, 8, 9, 16, 17])

@@ -258,6 +258,34 @@ def cpu_native_torch(torch, sample: int = 1 << 18) -> dict:
     }
 
 
+def small_batch_latency(torch, fh, device, iters: int = 400) -> dict:
+    """Host-bound latency at B=1, N=4 FP32 (the reference's small-batch comparison): wall time
+    per call, including launch and the autograd engine, averaged over back-to-back calls."""
+    x = torch.randn(1, 4, 4, device=device) * 0.25
+    g = torch.randn(1, 4, 4, device=device)
+    xg = x.clone().requires_grad_()
+
+    def per_call(fn):
+        for _ in range(50):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / iters * 1e6
+
+    return {
+        "unit": "us",
+        "fh_forward": per_call(lambda: fh.matrix_exp(x)),
+        "fh_forward_backward": per_call(lambda: torch.autograd.grad(fh.matrix_exp(xg), xg, g)),
+        "native_forward": per_call(lambda: torch.linalg.matrix_exp(x)),
+        "native_forward_backward": per_call(lambda: torch.autograd.grad(torch.linalg.matrix_exp(xg), xg, g)),
+        "trivial_op_forward_backward": per_call(lambda: torch.autograd.grad(xg * 2.0, xg, g)),
+        "shape": "[1,4,4] float32",
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -298,6 +326,9 @@ def main() -> int:
         torch.cuda.empty_cache()
 
     head = results.get("c2")
+    log("[bench] small-batch latency ...")
+    latency = small_batch_latency(torch, fh, device)
+    log(f"[bench] small-batch latency: {json.dumps(latency)}")
     line = {
         "metric": METRIC,
         "value": head["matrices_per_s_fwd_bwd"] if head else None,
@@ -340,6 +371,7 @@ def main() -> int:
         log("[bench] cpu baselines ...")
         line["cpu_baseline"] = cpu_oracle_baseline(torch)
         line["cpu_native_torch"] = cpu_native_torch(torch)
+    line["small_batch_latency"] = latency
     line["configs"] = results
     print(json.dumps(line), flush=True)
     return 0

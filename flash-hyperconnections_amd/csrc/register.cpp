@@ -9,9 +9,15 @@
 // bit to the C ABI of libflash_hypercons_hip.so on the current HIP stream.
 // No staging copies are made (the reference materialises FP32 contiguous
 // copies in prepare_matrix, csrc/matrix_exp.cu:35-44).
+//
+// The autograd kernel of _matrix_exp is registered here as well, so that an
+// eager forward + backward never enters Python below the call itself (the
+// reference registers it from Python, ops/matrix_exp/__init__.py:61-77).
 #include <Python.h>
 
 #include <ATen/ATen.h>
+#include <ATen/core/dispatch/Dispatcher.h>
+#include <torch/autograd.h>
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 #include <torch/library.h>
@@ -115,6 +121,80 @@ std::tuple<at::Tensor, at::Tensor> expm_params_hip(const at::Tensor& a, const st
   return {params, norms};
 }
 
+using MatrixExpOp = c10::TypedOperatorHandle<at::Tensor(const at::Tensor&)>;
+using FrechetOp = c10::TypedOperatorHandle<at::Tensor(const at::Tensor&, const at::Tensor&)>;
+
+const MatrixExpOp& matrix_exp_op() {
+  static const MatrixExpOp op =
+      c10::Dispatcher::singleton().findSchemaOrThrow("flash_hypercons::_matrix_exp", "").typed<at::Tensor(const at::Tensor&)>();
+  return op;
+}
+
+const FrechetOp& frechet_op() {
+  static const FrechetOp op = c10::Dispatcher::singleton()
+                                  .findSchemaOrThrow("flash_hypercons::_frechet", "")
+                                  .typed<at::Tensor(const at::Tensor&, const at::Tensor&)>();
+  return op;
+}
+
+// [[A, G], [0, A]] in FP32; exp of it holds L(A, G) in its top-right block.
+at::Tensor frechet_block(const at::Tensor& input, const at::Tensor& direction) {
+  const at::Tensor a = input.to(at::kFloat);
+  const at::Tensor g = direction.to(at::kFloat);
+  return at::cat({at::cat({a, g}, -1), at::cat({at::zeros_like(a), a}, -1)}, -2);
+}
+
+at::Tensor top_right(const at::Tensor& e, int64_t n, at::ScalarType dtype) {
+  return e.narrow(-2, 0, n).narrow(-1, n, n).to(dtype);
+}
+
+// Reference ops/matrix_exp/__init__.py:32-37: the native block exponential.
+at::Tensor frechet_reference(const at::Tensor& input, const at::Tensor& direction) {
+  return top_right(at::linalg_matrix_exp(frechet_block(input, direction)), input.size(-1), input.scalar_type());
+}
+
+// The same block through this operator (2N <= 32): differentiable, and its
+// own gradient is again the Frechet kernel.
+at::Tensor frechet_differentiable(const at::Tensor& input, const at::Tensor& direction) {
+  return top_right(matrix_exp_op().call(frechet_block(input, direction)), input.size(-1), input.scalar_type());
+}
+
+// Gradient of exp at A against G, L(A^T, G) (reference :65-74).  Forward-mode
+// tangents take the native block exponential, as the reference does; a
+// backward that builds a graph (create_graph=True) takes the differentiable
+// block through this operator; otherwise the Frechet kernel.  Tensors with a
+// __torch_dispatch__ (fake, functional, user subclasses) take the same
+// branches and reach their handlers through the dispatcher; Python-level
+// __torch_function__ overrides are not visible here (the reference checks
+// them in its Python backward, but the Python entry point already sends such
+// subclasses to the native exponential).
+at::Tensor exp_gradient(const at::Tensor& input, const at::Tensor& grad) {
+  const at::Tensor a = input.mT();
+  if (input._fw_grad(0).defined() || grad._fw_grad(0).defined()) return frechet_reference(a, grad);
+  if (at::GradMode::is_enabled()) {
+    return 2 * input.size(-1) <= 32 ? frechet_differentiable(a, grad) : frechet_reference(a, grad);
+  }
+  return frechet_op().call(a, grad);
+}
+
+class MatrixExpFunction : public torch::autograd::Function<MatrixExpFunction> {
+ public:
+  static at::Tensor forward(torch::autograd::AutogradContext* ctx, const at::Tensor& input) {
+    ctx->save_for_backward({input});
+    at::AutoDispatchBelowADInplaceOrView below;
+    return matrix_exp_op().call(input);
+  }
+
+  static torch::autograd::variable_list backward(torch::autograd::AutogradContext* ctx,
+                                                 torch::autograd::variable_list grads) {
+    const at::Tensor input = ctx->get_saved_variables()[0];
+    if (!grads[0].defined()) return {at::Tensor()};
+    return {exp_gradient(input, grads[0])};
+  }
+};
+
+at::Tensor matrix_exp_autograd(const at::Tensor& input) { return MatrixExpFunction::apply(input); }
+
 }  // namespace
 }  // namespace flash_hypercons
 
@@ -131,6 +211,8 @@ TORCH_LIBRARY_IMPL(flash_hypercons, CUDA, m) {
   m.impl("_expm_debug", &flash_hypercons::expm_debug_hip);
   m.impl("_expm_params", &flash_hypercons::expm_params_hip);
 }
+
+TORCH_LIBRARY_IMPL(flash_hypercons, Autograd, m) { m.impl("_matrix_exp", &flash_hypercons::matrix_exp_autograd); }
 
 static PyModuleDef module = {PyModuleDef_HEAD_INIT, "_C", nullptr, -1, nullptr};
 

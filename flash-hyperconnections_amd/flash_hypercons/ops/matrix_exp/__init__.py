@@ -110,17 +110,16 @@ def _frechet_differentiable(input: torch.Tensor, direction: torch.Tensor) -> tor
     return torch.ops.flash_hypercons._matrix_exp(block)[..., :n, n:].to(input.dtype)
 
 
-def _setup_context(ctx, inputs, output):
-    ctx.save_for_backward(inputs[0])
-
-
 def _backward(ctx, grad_output):
     """Reference :65-74: the gradient of exp at A against G is L(A^T, G).
 
     Tensor subclasses, modes and forward-mode tangents take the reference's
     native block exponential as in the reference; a backward that builds a
     graph (``create_graph=True``) takes the block exponential through this
-    operator (``_frechet_differentiable``) instead of the native one.
+    operator (``_frechet_differentiable``) instead of the native one.  The
+    operator's own autograd kernel is the C++ restatement of this function
+    (``csrc/register.cpp``, ``exp_gradient``); this one serves
+    ``_DualMatrixExp``.
     """
     (input,) = ctx.saved_tensors
     if (
@@ -134,7 +133,6 @@ def _backward(ctx, grad_output):
     return torch.ops.flash_hypercons._frechet(input.mT, grad_output)
 
 
-torch.library.register_autograd("flash_hypercons::_matrix_exp", _backward, setup_context=_setup_context)
 
 
 def _tangent(input: torch.Tensor, tangent: torch.Tensor) -> torch.Tensor:

@@ -14,7 +14,10 @@ Also reported in the same JSON line:
   autograd on the host cores (the reference's own CPU path), on a sample;
 * ``configs`` -- configs 3-5 (BF16 N=4 sweep, strided FP32 N=16, FP16 N=32 and
   the same shape in FP32) with their own rooflines (HBM for N=4, FP32 MFMA for
-  N>=16, where the flop count uses each matrix's own squaring count).
+  N>=16, where the flop count uses each matrix's own squaring count);
+* ``reference_table`` -- the reference's own benchmark (N = 4, 8, 16, 32 at
+  B = 65,536 FP32, wall time per direct-API call) beside its published A100
+  figures; ``small_batch_latency`` -- B = 1 wall time per call.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--only c2]
 """
@@ -286,6 +289,54 @@ def small_batch_latency(torch, fh, device, iters: int = 400) -> dict:
     }
 
 
+# The reference's published table (VALIDATION.md:84-95): A100 80GB PCIe, FP32, B = 65,536,
+# median wall time per direct-API call in microseconds.
+REFERENCE_A100_US = {
+    (4, "forward"): 22.83, (4, "forward_backward"): 164.22,
+    (8, "forward"): 58.21, (8, "forward_backward"): 208.52,
+    (16, "forward"): 370.30, (16, "forward_backward"): 1208.46,
+    (32, "forward"): 1948.02, (32, "forward_backward"): 8723.40,
+}
+
+
+def reference_table(torch, fh, device, batch: int = 65536, warmup: int = 5, repeat: int = 10, trials: int = 3) -> dict:
+    """The reference's own benchmark on this GPU (its benchmarks/matrix_exp.py:75-105 method):
+    seeded inputs randn*0.1 and grads randn*0.2, FP32, B = 65,536; per mode, warmup calls, then
+    trials of back-to-back direct-API calls with synchronization at trial boundaries only; median
+    of the per-call trial means.  Wall time includes Python selection, allocation and autograd."""
+    rows = []
+    for n in (4, 8, 16, 32):
+        seed = 9041 + n * 1000003 + batch * 3
+        torch.manual_seed(seed)
+        a = torch.randn(batch, n, n, device=device) * 0.1
+        g = torch.randn_like(a) * 0.2
+        for mode in ("forward", "forward_backward"):
+            x = a.detach().requires_grad_(mode == "forward_backward")
+
+            def call(x=x, mode=mode):
+                y = fh.matrix_exp(x)
+                if mode == "forward_backward":
+                    return torch.autograd.grad(y, x, g)[0]
+                return y
+
+            for _ in range(warmup):
+                call()
+            times = []
+            for _ in range(trials):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                for _ in range(repeat):
+                    call()
+                torch.cuda.synchronize()
+                times.append((time.perf_counter() - t0) * 1e6 / repeat)
+            us = statistics.median(times)
+            ref = REFERENCE_A100_US[(n, mode)]
+            rows.append({"n": n, "mode": mode, "median_us": us, "matrices_per_s": batch / us * 1e6,
+                         "reference_a100_us": ref, "reference_time_over_ours": ref / us})
+    return {"batch": batch, "dtype": "f32", "method": f"{warmup} warmup, {trials} trials x {repeat} calls, median",
+            "reference_source": "reference VALIDATION.md:84-95 (A100 80GB PCIe)", "rows": rows}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -326,6 +377,11 @@ def main() -> int:
         torch.cuda.empty_cache()
 
     head = results.get("c2")
+    log("[bench] reference table ...")
+    table = reference_table(torch, fh, device)
+    for row in table["rows"]:
+        log(f"[bench] reference table: n={row['n']:2} {row['mode']:16} {row['median_us']:9.1f} us "
+            f"(A100 {row['reference_a100_us']:8.1f} us, x{row['reference_time_over_ours']:.2f})")
     log("[bench] small-batch latency ...")
     latency = small_batch_latency(torch, fh, device)
     log(f"[bench] small-batch latency: {json.dumps(latency)}")
@@ -372,6 +428,7 @@ def main() -> int:
         line["cpu_baseline"] = cpu_oracle_baseline(torch)
         line["cpu_native_torch"] = cpu_native_torch(torch)
     line["small_batch_latency"] = latency
+    line["reference_table"] = table
     line["configs"] = results
     print(json.dumps(line), flush=True)
     return 0

@@ -56,6 +56,18 @@ fh::Operand make_operand(const void* data, const int64_t strides[3], int neg, in
   return op;
 }
 
+// The P = 16/32 kernels address one matrix through a buffer resource with
+// 32-bit offsets: its footprint ((n - 1) * (sr + sc) + 1 elements) must stay
+// below 2 GiB and its strides non-negative.  Other operands go to the
+// one-wavefront-per-matrix kernel, which indexes in 64 bits.
+bool tile_addressable(const fh::Operand& op, int n, int dtype) {
+  if (op.sr < 0 || op.sc < 0 || op.sb < 0) return false;
+  const int64_t limit = (int64_t{1} << 31) - 1;
+  const int64_t es = element_size(dtype);
+  if (op.sr > limit || op.sc > limit) return false;
+  return ((n - 1) * (op.sr + op.sc) + 1) * es <= limit;
+}
+
 int validate(const void* input, const int64_t* strides, int dtype, int64_t batch, int n, const void* out) {
   if (n < 2 || n > 32 || (dtype != FH_DTYPE_F32 && dtype != FH_DTYPE_BF16 && dtype != FH_DTYPE_F16) || batch < 0)
     return fail(FH_ERR_INVALID_ARGUMENT, kInputMessage);
@@ -93,8 +105,10 @@ int launch(const void* input, const int64_t input_strides[3], int input_neg, con
     err = fh::launch_p4(args, dtype, pair, stream);
   } else if (P == 8) {
     err = fh::launch_oct(args, dtype, pair, stream);
-  } else {
+  } else if (tile_addressable(args.x, n, dtype) && (!pair || tile_addressable(args.g, n, dtype))) {
     err = fh::launch_tile(args, dtype, P, pair, stream);
+  } else {
+    err = fh::launch_generic(args, dtype, P, pair, stream);
   }
   if (err != hipSuccess) return fail(FH_ERR_LAUNCH, std::string("kernel launch failed: ") + hipGetErrorString(err));
   g_error.clear();

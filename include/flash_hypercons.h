@@ -54,7 +54,10 @@ extern "C" {
                                 evaluation order; a checking aid, not a fast path */
 
 /* exp(X) for X = input viewed as [batch, n, n] with element strides
- * strides[0..2] (batch, row, column) and a lazy-negation flag.
+ * strides[0..2] (batch, row, column) and a lazy-negation flag.  Any int64
+ * strides are accepted; an operand whose single-matrix footprint exceeds
+ * 2 GiB (or has a negative stride) is computed by the 64-bit-indexed
+ * one-wavefront-per-matrix kernel when n > 8.
  * Replaces matrix_exp_cuda (csrc/matrix_exp.cu:80-82), the CUDA kernel of the
  * schema flash_hypercons::_matrix_exp(Tensor input) -> Tensor
  * (csrc/register.cpp:11, :16).  Rejects n outside [2, 32] and unknown dtypes

@@ -114,6 +114,27 @@ def test_negated_transposed_expanded_views(dtype, n):
         check_north_star(y, reference(a))
 
 
+@pytest.mark.parametrize("n", [4, 8, 9, 16, 32])
+def test_operand_spanning_more_than_2gib(n):
+    """A view whose single matrix spans > 2 GiB of storage (row stride 2^27 elements): the
+    P = 16/32 kernels' 32-bit buffer offsets cannot reach it, so the launcher takes the
+    64-bit-indexed kernel; N <= 8 kernels index in 64 bits themselves.  Results must match
+    the same matrices passed contiguously, to the north-star tolerance."""
+    row_stride = 1 << 27
+    batch = 3
+    storage = torch.zeros((n - 1) * row_stride + batch * n + n, device="cuda")
+    a = storage.as_strided((batch, n, n), (n, row_stride, 1))
+    a.copy_(torch.randn(batch, n, n, device="cuda") * 0.5)
+    g = torch.randn(batch, n, n, device="cuda")
+    dense = a.contiguous()
+    y = torch.ops.flash_hypercons._matrix_exp(a)
+    frechet = torch.ops.flash_hypercons._frechet(a, g)
+    check_north_star(y, reference(dense))
+    check_north_star(frechet, reference(dense, g), backward=True)
+    check_north_star(torch.ops.flash_hypercons._frechet(g, a), reference(g, dense), backward=True)
+    del storage, a
+
+
 def test_vjp_matches_central_difference():
     for n in (3, 4, 8, 16, 32):
         a = (torch.randn(2, n, n, device="cuda") * 0.03).requires_grad_()

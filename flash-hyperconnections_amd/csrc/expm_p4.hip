@@ -43,17 +43,6 @@ struct PM {
   M4 u;
 };
 
-// Row i of X.Y into c (four entries, k = 0..3 in order).
-__device__ __forceinline__ void mul_row(const M4& x, const M4& y, int i, float* c) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    float acc = __builtin_fmaf(x.v[4 * i], y.v[j], 0.f);
-    acc = __builtin_fmaf(x.v[4 * i + 1], y.v[4 + j], acc);
-    acc = __builtin_fmaf(x.v[4 * i + 2], y.v[8 + j], acc);
-    c[j] = __builtin_fmaf(x.v[4 * i + 3], y.v[12 + j], acc);
-  }
-}
-
 // Row i of the structured product (D1.D2, D1.U2 + U1.D2): the D and D.U sums
 // run in one k loop, U.D in a second, and the two U sums are added last
 // (csrc/MatrixExpSmall.cuh:27-49).

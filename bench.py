@@ -344,6 +344,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baselines")
     ap.add_argument("--only", default=None, help="comma list of configs (c2,c3,c4,c5,c5f32,p8)")
+    ap.add_argument("--extras", action="store_true",
+                    help="with --only: also run the reference table and the small-batch latency")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one device copy of exactly 64 MiB (profiler counter calibration)")
     args = ap.parse_args()
@@ -377,14 +379,17 @@ def main() -> int:
         torch.cuda.empty_cache()
 
     head = results.get("c2")
-    log("[bench] reference table ...")
-    table = reference_table(torch, fh, device)
-    for row in table["rows"]:
-        log(f"[bench] reference table: n={row['n']:2} {row['mode']:16} {row['median_us']:9.1f} us "
-            f"(A100 {row['reference_a100_us']:8.1f} us, x{row['reference_time_over_ours']:.2f})")
-    log("[bench] small-batch latency ...")
-    latency = small_batch_latency(torch, fh, device)
-    log(f"[bench] small-batch latency: {json.dumps(latency)}")
+    table = latency = None
+    if args.only is None or args.extras:
+        # Not part of --only runs, so that a profile of one config holds only its own launches.
+        log("[bench] reference table ...")
+        table = reference_table(torch, fh, device)
+        for row in table["rows"]:
+            log(f"[bench] reference table: n={row['n']:2} {row['mode']:16} {row['median_us']:9.1f} us "
+                f"(A100 {row['reference_a100_us']:8.1f} us, x{row['reference_time_over_ours']:.2f})")
+        log("[bench] small-batch latency ...")
+        latency = small_batch_latency(torch, fh, device)
+        log(f"[bench] small-batch latency: {json.dumps(latency)}")
     line = {
         "metric": METRIC,
         "value": head["matrices_per_s_fwd_bwd"] if head else None,
@@ -427,8 +432,9 @@ def main() -> int:
         log("[bench] cpu baselines ...")
         line["cpu_baseline"] = cpu_oracle_baseline(torch)
         line["cpu_native_torch"] = cpu_native_torch(torch)
-    line["small_batch_latency"] = latency
-    line["reference_table"] = table
+    if latency is not None:
+        line["small_batch_latency"] = latency
+        line["reference_table"] = table
     line["configs"] = results
     print(json.dumps(line), flush=True)
     return 0

@@ -13,9 +13,10 @@
 // Its A operand is row q of X block (I, K): the lane's own R registers when
 // K == J, else those of the lane 4 positions away; its B operand is column q
 // of Y block (K, J): own C registers when K == I, else those of the lane 8
-// away.  Each K step therefore takes every operand with one bank-masked DPP
-// row rotation (row_ror 4 / 12 for A, row_ror 8 for B; lanes whose block
-// already holds the operand keep their own value), and steps run K = 0, 1 in
+// away.  Each K step therefore takes its A operands with one bank-masked DPP
+// row rotation (row_ror 4 / 12; lanes whose block already holds the operand
+// keep their own value) and its B operands by selecting between the lane's own
+// registers and one row_ror 8 copy shared by both steps; steps run K = 0, 1 in
 // turn -- the products accumulate k = 0..7 in the reference's order from +0,
 // each step one exact FMA (csrc/MatrixExpSmall.cuh:31-33).  Left operands
 // reach the R layout through an LDS transpose of each block in place.
@@ -102,12 +103,20 @@ __device__ __forceinline__ Q a_operand(const Q& xr) {
   return r;
 }
 // B operands of block step K from the C layout of Y: banks with I != K (I is
-// bit 1 of the bank) take the lane 8 away.
-template <int K>
-__device__ __forceinline__ Q b_operand(const Q& yc) {
-  Q r;
+// bit 1 of the bank) take the lane 8 away.  Both steps select between the
+// lane's own registers and one full row_ror:8 copy.
+struct BPair {
+  Q k0, k1;
+};
+__device__ __forceinline__ BPair b_operands(const Q& yc) {
+  const bool upper = (__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) & 8) != 0;
+  BPair r;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) r.v[k] = K == 0 ? dpp_take<kRor8, 0xC>(yc.v[k]) : dpp_take<kRor8, 0x3>(yc.v[k]);
+  for (int k = 0; k < 4; ++k) {
+    const float far = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(yc.v[k]), kRor8, 0xF, 0xF, false));
+    r.k0.v[k] = upper ? far : yc.v[k];
+    r.k1.v[k] = upper ? yc.v[k] : far;
+  }
   return r;
 }
 
@@ -127,12 +136,13 @@ __device__ __forceinline__ Q chain(const Q& a0, const Q& b0, const Q& a1, const 
 template <bool Pair>
 __device__ __forceinline__ PQ<Pair> pmm(const PQ<Pair>& xr, const PQ<Pair>& yc) {
   const Q ad0 = a_operand<0>(xr.d), ad1 = a_operand<1>(xr.d);
-  const Q bd0 = b_operand<0>(yc.d), bd1 = b_operand<1>(yc.d);
+  const BPair bd = b_operands(yc.d);
   PQ<Pair> c;
-  c.d = chain(ad0, bd0, ad1, bd1);
+  c.d = chain(ad0, bd.k0, ad1, bd.k1);
   if constexpr (Pair) {
-    const Q u = chain(ad0, b_operand<0>(yc.u), ad1, b_operand<1>(yc.u));
-    const Q v = chain(a_operand<0>(xr.u), bd0, a_operand<1>(xr.u), bd1);
+    const BPair bu = b_operands(yc.u);
+    const Q u = chain(ad0, bu.k0, ad1, bu.k1);
+    const Q v = chain(a_operand<0>(xr.u), bd.k0, a_operand<1>(xr.u), bd.k1);
 #pragma unroll
     for (int r = 0; r < 4; ++r) c.u.v[r] = u.v[r] + v.v[r];
   }

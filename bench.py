@@ -68,6 +68,12 @@ def make_inputs(name: str, torch, device):
         x = base
         g = torch.randn(b, n, n)
         dtype, layout = torch.float32, "transposed view"
+    elif name == "c2s8":
+        # Not a BASELINE config: one GPU's share of config 2 sharded over 8 GPUs (B / 8).
+        b, n = 1 << 17, 4
+        x = torch.randn(b, n, n) * 0.25
+        g = torch.randn(b, n, n)
+        dtype, layout = torch.float32, "contiguous"
     elif name == "p8":
         # Not a BASELINE config: the P = 8 kernel (n = 5..8) at [262144, 8, 8] FP32, same
         # per-matrix scale law as config 5.
@@ -343,7 +349,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baselines")
-    ap.add_argument("--only", default=None, help="comma list of configs (c2,c3,c4,c5,c5f32,p8)")
+    ap.add_argument("--only", default=None, help="comma list of configs (c2,c3,c4,c5,c5f32,p8,c2s8)")
     ap.add_argument("--extras", action="store_true",
                     help="with --only: also run the reference table and the small-batch latency")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -370,7 +376,7 @@ def main() -> int:
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    configs = (args.only or "c2,c3,c4,c5,c5f32,p8").split(",")
+    configs = (args.only or "c2,c3,c4,c5,c5f32,p8,c2s8").split(",")
     results = {}
     for name in configs:
         log(f"[bench] {name} ...")

@@ -27,11 +27,11 @@
 //   maximum) whenever that estimate decides it exactly; the FP64 sequential
 //   column sums of the reference run only near a squaring boundary or for
 //   non-finite input;
-// * products accumulate into the MFMA accumulator that already holds the
-//   term added to them (B4 into A9 = B1.B5 + B4, B2 into T = B2 + ..), and
-//   the Frechet half D1.U2 + U1.D2 is one accumulation chain.
-// Evaluation order therefore differs from the reference's sequential FMA
-// chains (parity is by tolerance; s is bit-identical).
+// * the Frechet half D1.U2 + U1.D2 is one accumulation chain.
+// Each FP32 MFMA step equals an fmaf chain over its k terms in ascending
+// order, so results differ from the reference's sequential FMA chains only
+// through the order of the k terms within a product and that one U chain
+// (parity is by tolerance; s is bit-identical).
 #include "fh_kernels.h"
 
 namespace fh {
@@ -110,20 +110,22 @@ __device__ __forceinline__ Acc<P> mma(const Tm<P>& xt, const Tm<P>& y, Acc<P> ac
   return acc;
 }
 
-// (D1, U1).(D2, U2) + (Dc, Uc) = (D1.D2 + Dc, D1.U2 + U1.D2 + Uc).
-template <int P, bool Pair>
-__device__ __forceinline__ PTm<P, Pair> pmm(const PTm<P, Pair>& xt, const PTm<P, Pair>& y, const PTm<P, Pair>& c) {
-  PTm<P, Pair> out;
-  out.d = from_acc<P>(mma<P>(xt.d, y.d, to_acc<P>(c.d)));
-  if constexpr (Pair) out.u = from_acc<P>(mma<P>(xt.u, y.d, mma<P>(xt.d, y.u, to_acc<P>(c.u))));
-  return out;
-}
+// (D1, U1).(D2, U2) = (D1.D2, D1.U2 + U1.D2).
 template <int P, bool Pair>
 __device__ __forceinline__ PTm<P, Pair> pmm(const PTm<P, Pair>& xt, const PTm<P, Pair>& y) {
   PTm<P, Pair> out;
   const Acc<P> zero = {};
   out.d = from_acc<P>(mma<P>(xt.d, y.d, zero));
+#ifdef FH_SPLIT_U
+  if constexpr (Pair) {
+    const Tm<P> du = from_acc<P>(mma<P>(xt.d, y.u, zero));
+    const Tm<P> ud = from_acc<P>(mma<P>(xt.u, y.d, zero));
+#pragma unroll
+    for (int r = 0; r < TileCfg<P>::R; ++r) out.u.v[r] = du.v[r] + ud.v[r];
+  }
+#else
   if constexpr (Pair) out.u = from_acc<P>(mma<P>(xt.u, y.d, mma<P>(xt.d, y.u, zero)));
+#endif
   return out;
 }
 
@@ -169,30 +171,27 @@ __device__ __forceinline__ PTm<P, Pair> ptranspose(const PTm<P, Pair>& a, float*
   return t;
 }
 
-// base + B(K+1), B(K+1) = c0*I + c1*A + c2*A^2 + c3*A^3 + c6*A^6 (reference
-// csrc/MatrixExpSmall.cuh:268-281); zero coefficients skipped, identity on D
-// only (`dreg`: the VGPR of this lane's diagonal entry, -1 for none).
-template <int K, int P, bool Pair, bool Base>
+// B(K+1) = c0*I + c1*A + c2*A^2 + c3*A^3 + c6*A^6 (reference
+// csrc/MatrixExpSmall.cuh:268-281), the contracted chain with zero
+// coefficients skipped; identity on D only (`dreg`: the VGPR of this lane's
+// diagonal entry, -1 for none).
+template <int K, int P, bool Pair>
 __device__ __forceinline__ PTm<P, Pair> combine(const PTm<P, Pair>& a, const PTm<P, Pair>& a2,
-                                                const PTm<P, Pair>& a3, const PTm<P, Pair>& a6,
-                                                const PTm<P, Pair>& base, int dreg) {
+                                                const PTm<P, Pair>& a3, const PTm<P, Pair>& a6, int dreg) {
   using C = TileCfg<P>;
   constexpr float c0 = kCoef[K][0], c1 = kCoef[K][1], c2 = kCoef[K][2], c3 = kCoef[K][3], c6 = kCoef[K][4];
   PTm<P, Pair> b;
 #pragma unroll
   for (int r = 0; r < C::R; ++r) {
-    float t = Base ? base.d.v[r] : 0.f;
-    if constexpr (c0 != 0.f) {
-      const float id = dreg == r ? c0 : 0.f;
-      t = Base ? t + id : id;
-    }
+    float t = 0.f;
+    if constexpr (c0 != 0.f) t = dreg == r ? c0 : 0.f;
     if constexpr (c1 != 0.f) t = __builtin_fmaf(c1, a.d.v[r], t);
     t = __builtin_fmaf(c2, a2.d.v[r], t);
     t = __builtin_fmaf(c3, a3.d.v[r], t);
     if constexpr (c6 != 0.f) t = __builtin_fmaf(c6, a6.d.v[r], t);
     b.d.v[r] = t;
     if constexpr (Pair) {
-      float w = Base ? base.u.v[r] : 0.f;
+      float w = 0.f;
       if constexpr (c1 != 0.f) w = __builtin_fmaf(c1, a.u.v[r], w);
       w = __builtin_fmaf(c2, a2.u.v[r], w);
       w = __builtin_fmaf(c3, a3.u.v[r], w);
@@ -201,6 +200,17 @@ __device__ __forceinline__ PTm<P, Pair> combine(const PTm<P, Pair>& a, const PTm
     }
   }
   return b;
+}
+
+template <int P, bool Pair>
+__device__ __forceinline__ PTm<P, Pair> padd(const PTm<P, Pair>& x, const PTm<P, Pair>& y) {
+  PTm<P, Pair> z;
+#pragma unroll
+  for (int r = 0; r < TileCfg<P>::R; ++r) {
+    z.d.v[r] = x.d.v[r] + y.d.v[r];
+    if constexpr (Pair) z.u.v[r] = x.u.v[r] + y.u.v[r];
+  }
+  return z;
 }
 
 // Layout classes for loading: rows contiguous (kLoadRows) loads the D layout
@@ -436,12 +446,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kTileWaves<P
     const PTm<P, Pair> a2 = pmm<P, Pair>(at, a);
     const PTm<P, Pair> a3 = pmm<P, Pair>(at, a2);
     const PTm<P, Pair> a6 = pmm<P, Pair>(ptranspose<P, Pair>(a3, buf, lane), a3);
-    const PTm<P, Pair> none{};
-    PTm<P, Pair> a9 = pmm<P, Pair>(ptranspose<P, Pair>(combine<0, P, Pair, false>(a, a2, a3, a6, none, dreg), buf, lane),
-                                   combine<4, P, Pair, false>(a, a2, a3, a6, none, dreg),
-                                   combine<3, P, Pair, false>(a, a2, a3, a6, none, dreg));
-    const PTm<P, Pair> lhst = ptranspose<P, Pair>(combine<2, P, Pair, true>(a, a2, a3, a6, a9, dreg), buf, lane);
-    PTm<P, Pair> res = pmm<P, Pair>(lhst, a9, combine<1, P, Pair, false>(a, a2, a3, a6, none, dreg));
+    // The sums B1.B5 + B4, B3 + A9 and B2 + (..).A9 are formed after their
+    // products, as in the reference: starting the MFMA accumulations from B4
+    // and B2 instead raised the FP32 error 1.4-fold on average (measured over
+    // config 5 against the FP64 result and the reference's own arithmetic).
+    const PTm<P, Pair> a9 =
+        padd<P, Pair>(pmm<P, Pair>(ptranspose<P, Pair>(combine<0, P, Pair>(a, a2, a3, a6, dreg), buf, lane),
+                                   combine<4, P, Pair>(a, a2, a3, a6, dreg)),
+                      combine<3, P, Pair>(a, a2, a3, a6, dreg));
+    const PTm<P, Pair> lhst = ptranspose<P, Pair>(padd<P, Pair>(combine<2, P, Pair>(a, a2, a3, a6, dreg), a9), buf, lane);
+    PTm<P, Pair> res = padd<P, Pair>(combine<1, P, Pair>(a, a2, a3, a6, dreg), pmm<P, Pair>(lhst, a9));
     for (int i = 0; i < s; ++i) res = pmm<P, Pair>(ptranspose<P, Pair>(res, buf, lane), res);
 
     store_tile<T, P, Full>(args.out, b, n, lane, Pair ? res.u : res.d);

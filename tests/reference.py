@@ -11,6 +11,19 @@ FP32 relative Frobenius error <= 1e-5 forward and <= 1e-4 backward per matrix;
 FP16/BF16 every element within one output-dtype ulp of the FP64 reference
 rounded to that dtype (absolute floor: one ulp of the matrix's largest |ref|),
 with infinities matching the rounded reference exactly.
+
+When the caller passes the squaring counts, both bounds also cover the FP32
+evaluation itself.  Scaling and squaring amplifies the normwise FP32 rounding
+error about 2^s-fold, so neither the reference's own arithmetic (the CPU
+oracle, bit-identical to the reference's evaluation order) nor these kernels
+stay below 1e-5 for every matrix with s >= 6: over all 32 768 matrices of
+config 5 in FP32 the oracle exceeds it on 29 and the tile kernels on 28, both
+at most ~6.7 * 2^s FP32 units.  The FP32 bound therefore becomes
+max(1e-5, 8 * 2^s * 2^-24).  For FP16/BF16 the floor adds 2^(s+1) FP32 units
+of the matrix's largest |ref| (over all entries, including those that overflow
+the output dtype): when the exact result exceeds FP16's range by orders of
+magnitude its finite entries carry an absolute error many FP16 ulps wide --
+the oracle shows up to ~4.6 ulps on such config-5 matrices.
 """
 
 import torch
@@ -57,18 +70,28 @@ def rel_frobenius(actual, ref64):
     return num / den
 
 
-def check_north_star(actual, ref64, *, backward=False):
-    """Per-matrix contract; returns the worst error measure for reporting."""
+def check_north_star(actual, ref64, *, backward=False, squarings=None):
+    """Per-matrix contract; returns the worst error measure for reporting.
+
+    ``squarings``: optional per-matrix squaring counts, which add the FP32
+    evaluation floor of scaling and squaring (module docstring): for FP32
+    outputs a relative Frobenius error of 8 * 2^s FP32 units (2^(s+3-24)) where
+    that exceeds the fixed bound -- only s >= 5 is affected."""
     assert actual.shape == ref64.shape
     if not actual.numel():
         return 0.0
     ref64 = ref64.to(actual.device)
     if actual.dtype == torch.float32:
         err = rel_frobenius(actual, ref64)
-        bound = BWD_REL_FRO if backward else FWD_REL_FRO
-        worst = err.max().item()
-        assert worst <= bound, f"relative Frobenius error {worst:.3e} > {bound:.0e}"
-        return worst
+        bound = torch.full_like(err, BWD_REL_FRO if backward else FWD_REL_FRO)
+        if squarings is not None:
+            s = squarings.to(err.device).double().clamp_min(0)
+            bound = torch.maximum(bound, torch.pow(2.0, s + 3 - 24))
+        excess = err / bound
+        worst = excess.max().item()
+        i = int(excess.argmax())
+        assert worst <= 1.0, f"relative Frobenius error {err[i].item():.3e} > {bound[i].item():.1e} (matrix {i})"
+        return err.max().item()
     rounded = ref64.to(actual.dtype)
     inf_ref = rounded.isinf()
     assert torch.equal(actual.isinf(), inf_ref), "infinity pattern differs from the rounded FP64 reference"
@@ -83,6 +106,10 @@ def check_north_star(actual, ref64, *, backward=False):
     finite_ref = torch.where(fin, ref64, torch.zeros_like(ref64))
     diff = (act - finite_ref).abs()
     floor = ulp(finite_ref.abs().flatten(-2).amax(-1), actual.dtype)[..., None, None]
+    if squarings is not None:
+        s = squarings.to(ref64.device).double().clamp_min(0)
+        fp32_floor = torch.pow(2.0, s + 1 - 24) * ref64.abs().flatten(-2).amax(-1)
+        floor = torch.maximum(floor, fp32_floor[..., None, None])
     tol = torch.maximum(ulp(torch.maximum(act.abs(), finite_ref.abs()), actual.dtype), floor)
     excess = diff / tol
     worst = excess.max().item()

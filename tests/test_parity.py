@@ -159,3 +159,48 @@ def test_squaring_boundary_fixture_on_gpu(n):
     assert params[:, 1].cpu().tolist() == d[f"s{n}"].tolist()
     _, s = run_kernel(x, None, AUTO)
     assert s.cpu().tolist() == d[f"s{n}"].tolist()
+
+
+def _baseline_inputs(name):
+    """BASELINE configs 2-5 at their full shapes (bench.py's seeded generators)."""
+    import bench
+
+    x, g, _ = bench.make_inputs(name, torch, "cuda")
+    return x, g
+
+
+@pytest.mark.parametrize("name", ["c2", "c3", "c4", "c5", "c5f32"])
+def test_full_size_configs_sampled(name):
+    """Size-independent properties at BASELINE sizes: a matrix's result does not depend on
+    the batch around it (bit for bit, forward and Frechet), its squaring count matches the
+    oracle's, and the sampled results meet the north-star tolerances against FP64."""
+    x, g = _baseline_inputs(name)
+    b = x.shape[0]
+    xt = x.mT
+    y, s_fwd = run_kernel(x, None, AUTO)
+    d, s_bwd = run_kernel(xt, g, AUTO)
+    gen = torch.Generator().manual_seed(7)
+    idx = torch.cat((torch.randint(0, b, (192,), generator=gen), torch.arange(b - 64, b))).unique()
+    idx_dev = idx.to(x.device)
+    xs, gs, xts = x[idx_dev], g[idx_dev], xt[idx_dev]
+    y_small, _ = run_kernel(xs, None, AUTO)
+    d_small, _ = run_kernel(xts, gs, AUTO)
+    assert torch.equal(y[idx_dev], y_small)
+    assert torch.equal(d[idx_dev], d_small)
+    o_fwd, s_ref = oracle_result(xs, None)
+    o_bwd, s_ref_b = oracle_result(xts, gs)
+    assert torch.equal(s_fwd[idx_dev].cpu().to(s_ref.dtype), s_ref)
+    assert torch.equal(s_bwd[idx_dev].cpu().to(s_ref_b.dtype), s_ref_b)
+    finite = s_ref >= 0
+    finite_b = s_ref_b >= 0
+    f, fb = finite.to(x.device), finite_b.to(x.device)
+    check_north_star(y_small[f], reference(xs[f]), squarings=s_ref[finite])
+    check_north_star(d_small[fb], reference(xts[fb], gs[fb]), backward=True, squarings=s_ref_b[finite_b])
+    # The tile kernels' FP32 error matches the reference arithmetic's: compare means.
+    if x.dtype == torch.float32:
+        for out, ora, ref in ((y_small[f], o_fwd[finite], reference(xs[f])),
+                              (d_small[fb], o_bwd[finite_b], reference(xts[fb], gs[fb]))):
+            from tests.reference import rel_frobenius
+
+            ratio = rel_frobenius(out, ref).mean() / rel_frobenius(ora.to(out.device), ref).mean()
+            assert ratio <= 1.25, f"mean FP32 error {ratio:.2f}x the reference arithmetic's"

@@ -200,3 +200,34 @@ def test_invalid_direct_calls_raise_reference_messages():
         torch.ops.flash_hypercons._matrix_exp(torch.randn(2, 4, 4, device="cuda", dtype=torch.float64))
     with pytest.raises(RuntimeError, match="direction must match"):
         torch.ops.flash_hypercons._frechet(torch.randn(2, 4, 4, device="cuda"), torch.randn(2, 5, 5, device="cuda"))
+
+
+@pytest.mark.parametrize("n", [4, 8, 16, 32])
+def test_graph_capture_replays_match_eager(n):
+    """The launches allocate nothing and issue no memsets, so forward + Frechet can be captured
+    in a HIP graph; every replay (with eager work in between) equals the eager result bit for bit."""
+    torch.manual_seed(n)
+    x = torch.randn(300, n, n, device="cuda") * 0.4
+    g = torch.randn(300, n, n, device="cuda")
+    eager_y = torch.ops.flash_hypercons._matrix_exp(x)
+    eager_d = torch.ops.flash_hypercons._frechet(x.mT, g)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(2):  # warm-up on the capture stream
+            torch.ops.flash_hypercons._matrix_exp(x)
+            torch.ops.flash_hypercons._frechet(x.mT, g)
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y = torch.ops.flash_hypercons._matrix_exp(x)
+        d = torch.ops.flash_hypercons._frechet(x.mT, g)
+    for replay in range(3):
+        y.zero_()
+        d.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager_y), f"replay {replay}"
+        assert torch.equal(d, eager_d), f"replay {replay}"
+        torch.ops.flash_hypercons._matrix_exp(g)  # unrelated eager work between replays

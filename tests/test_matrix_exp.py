@@ -231,3 +231,15 @@ def test_graph_capture_replays_match_eager(n):
         assert torch.equal(y, eager_y), f"replay {replay}"
         assert torch.equal(d, eager_d), f"replay {replay}"
         torch.ops.flash_hypercons._matrix_exp(g)  # unrelated eager work between replays
+
+
+@pytest.mark.skipif(torch.cuda.device_count() < 2, reason="needs a second GPU (these boxes have one)")
+def test_input_on_noncurrent_device():
+    """The launch runs on the input's device under a device guard and restores the current one
+    (reference tests/test_matrix_exp.py:143-149)."""
+    torch.cuda.set_device(0)
+    a = torch.randn(2, 4, 4, device="cuda:1") * 0.1
+    y = fh.matrix_exp(a)
+    assert torch.cuda.current_device() == 0
+    assert y.device == a.device
+    check_north_star(y, reference(a))

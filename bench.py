@@ -242,8 +242,12 @@ def cpu_native_torch(torch, sample: int = 1 << 18) -> dict:
     threads = torch.get_num_threads()
     y = torch.linalg.matrix_exp(x[:1024])  # warm
     torch.autograd.grad(y.sum(), x)
-    times = []
+    times, fwd_times = [], []
     for _ in range(3):
+        t0 = time.perf_counter()
+        with torch.no_grad():
+            torch.linalg.matrix_exp(x)
+        fwd_times.append(time.perf_counter() - t0)
         t0 = time.perf_counter()
         y = torch.linalg.matrix_exp(x)
         torch.autograd.grad(y, x, g)
@@ -259,11 +263,13 @@ def cpu_native_torch(torch, sample: int = 1 << 18) -> dict:
         pass
     return {
         "value": sample / dt,
+        "forward_value": sample / statistics.median(fwd_times),
         "unit": "matrices/s",
         "cores": threads,
         "cpu_count": os.cpu_count(),
         "cpu_model": model,
-        "sample": f"first {sample} config-2 matrices, torch.linalg.matrix_exp + autograd.grad, median of 3",
+        "sample": f"first {sample} config-2 matrices, torch.linalg.matrix_exp + autograd.grad "
+        f"(value) and forward alone (forward_value), median of 3",
     }
 
 

@@ -116,16 +116,7 @@ __device__ __forceinline__ PTm<P, Pair> pmm(const PTm<P, Pair>& xt, const PTm<P,
   PTm<P, Pair> out;
   const Acc<P> zero = {};
   out.d = from_acc<P>(mma<P>(xt.d, y.d, zero));
-#ifdef FH_SPLIT_U
-  if constexpr (Pair) {
-    const Tm<P> du = from_acc<P>(mma<P>(xt.d, y.u, zero));
-    const Tm<P> ud = from_acc<P>(mma<P>(xt.u, y.d, zero));
-#pragma unroll
-    for (int r = 0; r < TileCfg<P>::R; ++r) out.u.v[r] = du.v[r] + ud.v[r];
-  }
-#else
   if constexpr (Pair) out.u = from_acc<P>(mma<P>(xt.u, y.d, mma<P>(xt.d, y.u, zero)));
-#endif
   return out;
 }
 
@@ -171,20 +162,38 @@ __device__ __forceinline__ PTm<P, Pair> ptranspose(const PTm<P, Pair>& a, float*
   return t;
 }
 
+// c0*I in the D layout for the two combines with an identity term (B3 and B4,
+// reference csrc/MatrixExpSmall.cuh:268-281); `dreg` is the VGPR of this
+// lane's diagonal entry, -1 for none.
+template <int P>
+struct Ident {
+  Tm<P> b3, b4;
+};
+template <int P>
+__device__ __forceinline__ Ident<P> make_ident(int dreg) {
+  Ident<P> id;
+#pragma unroll
+  for (int r = 0; r < TileCfg<P>::R; ++r) {
+    id.b3.v[r] = dreg == r ? kCoef[2][0] : 0.f;
+    id.b4.v[r] = dreg == r ? kCoef[3][0] : 0.f;
+  }
+  return id;
+}
+
 // B(K+1) = c0*I + c1*A + c2*A^2 + c3*A^3 + c6*A^6 (reference
 // csrc/MatrixExpSmall.cuh:268-281), the contracted chain with zero
-// coefficients skipped; identity on D only (`dreg`: the VGPR of this lane's
-// diagonal entry, -1 for none).
+// coefficients skipped; the identity term (D only) comes from `id`.
 template <int K, int P, bool Pair>
 __device__ __forceinline__ PTm<P, Pair> combine(const PTm<P, Pair>& a, const PTm<P, Pair>& a2,
-                                                const PTm<P, Pair>& a3, const PTm<P, Pair>& a6, int dreg) {
+                                                const PTm<P, Pair>& a3, const PTm<P, Pair>& a6, const Ident<P>& id) {
   using C = TileCfg<P>;
   constexpr float c0 = kCoef[K][0], c1 = kCoef[K][1], c2 = kCoef[K][2], c3 = kCoef[K][3], c6 = kCoef[K][4];
+  static_assert(c0 == 0.f || K == 2 || K == 3, "identity terms are B3 and B4");
   PTm<P, Pair> b;
 #pragma unroll
   for (int r = 0; r < C::R; ++r) {
     float t = 0.f;
-    if constexpr (c0 != 0.f) t = dreg == r ? c0 : 0.f;
+    if constexpr (c0 != 0.f) t = K == 2 ? id.b3.v[r] : id.b4.v[r];
     if constexpr (c1 != 0.f) t = __builtin_fmaf(c1, a.d.v[r], t);
     t = __builtin_fmaf(c2, a2.d.v[r], t);
     t = __builtin_fmaf(c3, a3.d.v[r], t);
@@ -387,11 +396,25 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kTileWaves<P
     if constexpr (Pair) ng = load_raw<T, P, Full>(sg, b, n, lane);
   }
   const int dreg_lane = C::diag_reg(lane);
+  // P = 16 keeps the 2R identity values in registers for the whole kernel (it
+  // has registers to spare); P = 32 re-forms them per matrix.
+  Ident<P> id_lane;
+  if constexpr (P == 16) {
+    id_lane = make_ident<P>(dreg_lane);
+#pragma unroll
+    for (int r = 0; r < R; ++r) asm volatile("" : "+v"(id_lane.b3.v[r]), "+v"(id_lane.b4.v[r]));
+  }
   for (; b < args.batch; b += gridDim.x) {
-    // Opaque per matrix so that the identity terms are selected where they
-    // are used instead of being kept live as 2R registers across the loop.
-    int dreg = dreg_lane;
-    asm volatile("" : "+v"(dreg));
+    // For P = 32, opaque per matrix so that the identity terms are selected
+    // where they are used instead of being kept live across the loop.
+    Ident<P> id;
+    if constexpr (P == 16) {
+      id = id_lane;
+    } else {
+      int dreg = dreg_lane;
+      asm volatile("" : "+v"(dreg));
+      id = make_ident<P>(dreg);
+    }
     const Tm<P> lx = to_tile<T, P>(nx);
     Tm<P> lg;
     if constexpr (Pair) lg = to_tile<T, P>(ng);
@@ -451,11 +474,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kTileWaves<P
     // and B2 instead raised the FP32 error 1.4-fold on average (measured over
     // config 5 against the FP64 result and the reference's own arithmetic).
     const PTm<P, Pair> a9 =
-        padd<P, Pair>(pmm<P, Pair>(ptranspose<P, Pair>(combine<0, P, Pair>(a, a2, a3, a6, dreg), buf, lane),
-                                   combine<4, P, Pair>(a, a2, a3, a6, dreg)),
-                      combine<3, P, Pair>(a, a2, a3, a6, dreg));
-    const PTm<P, Pair> lhst = ptranspose<P, Pair>(padd<P, Pair>(combine<2, P, Pair>(a, a2, a3, a6, dreg), a9), buf, lane);
-    PTm<P, Pair> res = padd<P, Pair>(combine<1, P, Pair>(a, a2, a3, a6, dreg), pmm<P, Pair>(lhst, a9));
+        padd<P, Pair>(pmm<P, Pair>(ptranspose<P, Pair>(combine<0, P, Pair>(a, a2, a3, a6, id), buf, lane),
+                                   combine<4, P, Pair>(a, a2, a3, a6, id)),
+                      combine<3, P, Pair>(a, a2, a3, a6, id));
+    const PTm<P, Pair> lhst = ptranspose<P, Pair>(padd<P, Pair>(combine<2, P, Pair>(a, a2, a3, a6, id), a9), buf, lane);
+    PTm<P, Pair> res = padd<P, Pair>(combine<1, P, Pair>(a, a2, a3, a6, id), pmm<P, Pair>(lhst, a9));
     for (int i = 0; i < s; ++i) res = pmm<P, Pair>(ptranspose<P, Pair>(res, buf, lane), res);
 
     store_tile<T, P, Full>(args.out, b, n, lane, Pair ? res.u : res.d);

@@ -27,7 +27,9 @@
 //   maximum) whenever that estimate decides it exactly; the FP64 sequential
 //   column sums of the reference run only near a squaring boundary or for
 //   non-finite input;
-// * the Frechet half D1.U2 + U1.D2 is one accumulation chain.
+// * the Frechet half D1.U2 + U1.D2 is one accumulation chain, fed step by
+//   step together with the D chain (two independent MFMA chains, and each
+//   operand register dies after its step).
 // Each FP32 MFMA step equals an fmaf chain over its k terms in ascending
 // order, so results differ from the reference's sequential FMA chains only
 // through the order of the k terms within a product and that one U chain
@@ -110,13 +112,23 @@ __device__ __forceinline__ Acc<P> mma(const Tm<P>& xt, const Tm<P>& y, Acc<P> ac
   return acc;
 }
 
-// (D1, U1).(D2, U2) = (D1.D2, D1.U2 + U1.D2).
+// (D1, U1).(D2, U2) = (D1.D2, D1.U2 + U1.D2).  Step r feeds all three
+// products, so each operand register dies after its step and the D and U
+// accumulations alternate as two independent MFMA chains.
 template <int P, bool Pair>
 __device__ __forceinline__ PTm<P, Pair> pmm(const PTm<P, Pair>& xt, const PTm<P, Pair>& y) {
+  Acc<P> d = {}, u = {};
+#pragma unroll
+  for (int r = 0; r < TileCfg<P>::R; ++r) {
+    d = TileCfg<P>::mfma(xt.d.v[r], y.d.v[r], d);
+    if constexpr (Pair) {
+      u = TileCfg<P>::mfma(xt.d.v[r], y.u.v[r], u);
+      u = TileCfg<P>::mfma(xt.u.v[r], y.d.v[r], u);
+    }
+  }
   PTm<P, Pair> out;
-  const Acc<P> zero = {};
-  out.d = from_acc<P>(mma<P>(xt.d, y.d, zero));
-  if constexpr (Pair) out.u = from_acc<P>(mma<P>(xt.u, y.d, mma<P>(xt.d, y.u, zero)));
+  out.d = from_acc<P>(d);
+  if constexpr (Pair) out.u = from_acc<P>(u);
   return out;
 }
 
@@ -163,19 +175,31 @@ __device__ __forceinline__ PTm<P, Pair> ptranspose(const PTm<P, Pair>& a, float*
 }
 
 // c0*I in the D layout for the two combines with an identity term (B3 and B4,
-// reference csrc/MatrixExpSmall.cuh:268-281); `dreg` is the VGPR of this
-// lane's diagonal entry, -1 for none.
+// reference csrc/MatrixExpSmall.cuh:268-281), from `dreg`, the VGPR of this
+// lane's diagonal entry (-1 for none).  P = 16 keeps the 2R values in
+// registers for the whole kernel (it has registers to spare); P = 32 selects
+// them where they are used.
 template <int P>
 struct Ident {
-  Tm<P> b3, b4;
+  int dreg;
+  __device__ __forceinline__ float value(int k, int r) const { return dreg == r ? kCoef[k][0] : 0.f; }
+};
+template <>
+struct Ident<16> {
+  Tm<16> b3, b4;
+  __device__ __forceinline__ float value(int k, int r) const { return k == 2 ? b3.v[r] : b4.v[r]; }
 };
 template <int P>
 __device__ __forceinline__ Ident<P> make_ident(int dreg) {
   Ident<P> id;
+  if constexpr (P == 16) {
 #pragma unroll
-  for (int r = 0; r < TileCfg<P>::R; ++r) {
-    id.b3.v[r] = dreg == r ? kCoef[2][0] : 0.f;
-    id.b4.v[r] = dreg == r ? kCoef[3][0] : 0.f;
+    for (int r = 0; r < TileCfg<P>::R; ++r) {
+      id.b3.v[r] = dreg == r ? kCoef[2][0] : 0.f;
+      id.b4.v[r] = dreg == r ? kCoef[3][0] : 0.f;
+    }
+  } else {
+    id.dreg = dreg;
   }
   return id;
 }
@@ -193,7 +217,7 @@ __device__ __forceinline__ PTm<P, Pair> combine(const PTm<P, Pair>& a, const PTm
 #pragma unroll
   for (int r = 0; r < C::R; ++r) {
     float t = 0.f;
-    if constexpr (c0 != 0.f) t = K == 2 ? id.b3.v[r] : id.b4.v[r];
+    if constexpr (c0 != 0.f) t = id.value(K, r);
     if constexpr (c1 != 0.f) t = __builtin_fmaf(c1, a.d.v[r], t);
     t = __builtin_fmaf(c2, a2.d.v[r], t);
     t = __builtin_fmaf(c3, a3.d.v[r], t);
@@ -396,8 +420,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kTileWaves<P
     if constexpr (Pair) ng = load_raw<T, P, Full>(sg, b, n, lane);
   }
   const int dreg_lane = C::diag_reg(lane);
-  // P = 16 keeps the 2R identity values in registers for the whole kernel (it
-  // has registers to spare); P = 32 re-forms them per matrix.
   Ident<P> id_lane;
   if constexpr (P == 16) {
     id_lane = make_ident<P>(dreg_lane);
@@ -473,12 +495,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kTileWaves<P
     // products, as in the reference: starting the MFMA accumulations from B4
     // and B2 instead raised the FP32 error 1.4-fold on average (measured over
     // config 5 against the FP64 result and the reference's own arithmetic).
-    const PTm<P, Pair> a9 =
-        padd<P, Pair>(pmm<P, Pair>(ptranspose<P, Pair>(combine<0, P, Pair>(a, a2, a3, a6, id), buf, lane),
-                                   combine<4, P, Pair>(a, a2, a3, a6, id)),
-                      combine<3, P, Pair>(a, a2, a3, a6, id));
+    const PTm<P, Pair> b1t = ptranspose<P, Pair>(combine<0, P, Pair>(a, a2, a3, a6, id), buf, lane);
+    const PTm<P, Pair> b5 = combine<4, P, Pair>(a, a2, a3, a6, id);
+    const PTm<P, Pair> b1b5 = pmm<P, Pair>(b1t, b5);
+    const PTm<P, Pair> a9 = padd<P, Pair>(b1b5, combine<3, P, Pair>(a, a2, a3, a6, id));
     const PTm<P, Pair> lhst = ptranspose<P, Pair>(padd<P, Pair>(combine<2, P, Pair>(a, a2, a3, a6, id), a9), buf, lane);
-    PTm<P, Pair> res = padd<P, Pair>(combine<1, P, Pair>(a, a2, a3, a6, id), pmm<P, Pair>(lhst, a9));
+    const PTm<P, Pair> b2 = combine<1, P, Pair>(a, a2, a3, a6, id);
+    PTm<P, Pair> res = padd<P, Pair>(b2, pmm<P, Pair>(lhst, a9));
     for (int i = 0; i < s; ++i) res = pmm<P, Pair>(ptranspose<P, Pair>(res, buf, lane), res);
 
     store_tile<T, P, Full>(args.out, b, n, lane, Pair ? res.u : res.d);

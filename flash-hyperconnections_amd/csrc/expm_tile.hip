@@ -367,30 +367,35 @@ __device__ __forceinline__ float norm_estimate(const PTm<P, Pair>& a) {
 // The reference's FP64 norm (csrc/MatrixExpSmall.cuh:343-357): per column the
 // rows summed sequentially, |A| then |G| per row, then the column maximum; the
 // total of the column sums is finite exactly when every entry is (non-finite
-// rule, :318-331).  Returns false for non-finite input.
+// rule, :318-331), i.e. when every column sum is.  Returns false for
+// non-finite input.  This path is rare, so it is written for few live
+// registers: the row loop is not unrolled, and the maximum over columns reads
+// each lane's sum into scalar registers (the order of a maximum is free).
 template <int P, bool Pair>
-__device__ __forceinline__ bool exact_squarings(const PTm<P, Pair>& a, float* buf, double* colsum,
-                                                          int lane, int& s) {
+__device__ __forceinline__ bool exact_squarings(const PTm<P, Pair>& a, float* buf, int lane, int& s) {
   constexpr int LD = P + 1;
   tile_write<P>(a.d, buf, lane);
   if constexpr (Pair) tile_write<P>(a.u, buf + P * LD, lane);
   lds_order();
+  double v = 0.;
   if (lane < P) {
-    double v = 0.;
+#pragma unroll 1
     for (int row = 0; row < P; ++row) {
       v += fabs(static_cast<double>(buf[row * LD + lane]));
       if constexpr (Pair) v += fabs(static_cast<double>(buf[P * LD + row * LD + lane]));
     }
-    colsum[lane] = v;
   }
   lds_order();
-  double norm = 0., total = 0.;
+  if (__builtin_amdgcn_ballot_w64(!__builtin_isfinite(v)) != 0) return false;
+  double norm = 0.;
+  const uint64_t bits = __builtin_bit_cast(uint64_t, v);
+  const int vlo = static_cast<int>(bits), vhi = static_cast<int>(bits >> 32);
+#pragma unroll 1
   for (int j = 0; j < P; ++j) {
-    norm = fmax(norm, colsum[j]);
-    total += colsum[j];
+    const uint64_t w = static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(vlo, j))) |
+                       (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(vhi, j))) << 32);
+    norm = fmax(norm, __builtin_bit_cast(double, w));
   }
-  lds_order();
-  if (!__builtin_isfinite(total)) return false;
   s = squarings_from_norm(norm);
   return true;
 }
@@ -407,7 +412,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kTileWaves<P
   using C = TileCfg<P>;
   constexpr int R = C::R;
   __shared__ float buf[2 * P * (P + 1)];
-  __shared__ double colsum[P];
   const int lane = threadIdx.x;
   const int n = Full ? P : args.n;
   const TileSrc sx = make_src<T, P>(args.x, XL, n, lane);
@@ -461,7 +465,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kTileWaves<P
     }
 
     int s;
-    if (!squarings_from_estimate(norm_estimate<P, Pair>(a), s) && !exact_squarings<P, Pair>(a, buf, colsum, lane, s)) {
+    if (!squarings_from_estimate(norm_estimate<P, Pair>(a), s) && !exact_squarings<P, Pair>(a, buf, lane, s)) {
       // Non-finite entry: the whole matrix is NaN (csrc/MatrixExpSmall.cuh:318-331).
       Tm<P> nan;
 #pragma unroll

@@ -444,9 +444,18 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kTileWaves<P
     const Tm<P> lx = to_tile<T, P>(nx);
     Tm<P> lg;
     if constexpr (Pair) lg = to_tile<T, P>(ng);
+    // n < P = 32: the per-VGPR bounds predicates and offsets are formed
+    // afresh for each matrix from an opaque copy of the lane's offsets, so
+    // that they are not kept live across the loop (2R-3R registers these
+    // kernels do not have; P = 16 keeps them).
+    TileSrc sxm = sx, sgm = sg;
+    int lane_m = lane;
+    if constexpr (!Full && P == 32) {
+      asm volatile("" : "+v"(sxm.lane_off), "+v"(sgm.lane_off), "+v"(lane_m));
+    }
     if (b + gridDim.x < args.batch) {
-      nx = load_raw<T, P, Full>(sx, b + gridDim.x, n, lane);
-      if constexpr (Pair) ng = load_raw<T, P, Full>(sg, b + gridDim.x, n, lane);
+      nx = load_raw<T, P, Full>(sxm, b + gridDim.x, n, lane_m);
+      if constexpr (Pair) ng = load_raw<T, P, Full>(sgm, b + gridDim.x, n, lane_m);
     }
 
     // Both layouts of X (and G): the loaded one and its LDS transpose.
@@ -470,7 +479,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kTileWaves<P
       Tm<P> nan;
 #pragma unroll
       for (int r = 0; r < R; ++r) nan.v[r] = __builtin_nanf("");
-      store_tile<T, P, Full>(args.out, b, n, lane, nan);
+      store_tile<T, P, Full>(args.out, b, n, lane_m, nan);
       if (lane == 0 && args.s_out) args.s_out[b] = -1;
       continue;
     }
@@ -508,7 +517,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kTileWaves<P
     PTm<P, Pair> res = padd<P, Pair>(b2, pmm<P, Pair>(lhst, a9));
     for (int i = 0; i < s; ++i) res = pmm<P, Pair>(ptranspose<P, Pair>(res, buf, lane), res);
 
-    store_tile<T, P, Full>(args.out, b, n, lane, Pair ? res.u : res.d);
+    store_tile<T, P, Full>(args.out, b, n, lane_m, Pair ? res.u : res.d);
     if (lane == 0 && args.s_out) args.s_out[b] = s;
   }
 }

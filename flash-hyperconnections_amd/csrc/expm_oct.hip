@@ -4,22 +4,22 @@
 // Layout: an 8 x 8 matrix is a 2 x 2 arrangement of 4 x 4 blocks spread over
 // one row of 16 lanes: lane l serves matrix slot m = l/16, block (I, J) with
 // I = bit 3 and J = bit 2 of l, and index q = l%4 inside the block.  A
-// matrix value is held in one of two layouts of four VGPRs:
-//   C (columns): v[r] = M[4I + r][4J + q]      R (rows): v[k] = M[4I + q][4J + k].
+// matrix value is held in the C (column) layout of four VGPRs,
+//   v[r] = M[4I + r][4J + q],
+// and a left operand of a product as a whole row of eight VGPRs,
+//   v[k] = M[4I + q][k],  k = 0..7.
 // The 4x4x1 MFMA multiplies 16 independent 4 x 4 blocks per instruction
 // (block b's lanes supply A[i][0] from lane 4b+i and B[0][j] from lane 4b+j;
 // D[i][j] lands in lane 4b+j, VGPR i), so output block (I, J) of X.Y is
 //   sum over K = 0, 1 and k = 0..3 of  X_IK[:, k] (x) Y_KJ[k, :].
-// Its A operand is row q of X block (I, K): the lane's own R registers when
-// K == J, else those of the lane 4 positions away; its B operand is column q
-// of Y block (K, J): own C registers when K == I, else those of the lane 8
-// away.  Each K step therefore takes its A operands with one bank-masked DPP
-// row rotation (row_ror 4 / 12; lanes whose block already holds the operand
-// keep their own value) and its B operands by selecting between the lane's own
-// registers and one row_ror 8 copy shared by both steps; steps run K = 0, 1 in
-// turn -- the products accumulate k = 0..7 in the reference's order from +0,
-// each step one exact FMA (csrc/MatrixExpSmall.cuh:31-33).  Left operands
-// reach the R layout through an LDS transpose of each block in place.
+// Its A operand is row q of X block (I, K), entries 4K..4K+3 of the lane's
+// own row registers; its B operand is column q of Y block (K, J): own C
+// registers when K == I, else those of the lane 8 away, a select between the
+// lane's own registers and one row_ror 8 DPP copy shared by both steps.
+// Steps run K = 0, 1 in turn -- the products accumulate k = 0..7 in the
+// reference's order from +0, each step one exact FMA (csrc/MatrixExpSmall.cuh:
+// 31-33).  Rows are formed from the C layout through the wavefront's LDS plane
+// (one 16-byte write and eight reads per lane).
 //
 // Arithmetic is the reference's, element by element (csrc/MatrixExpSmall.cuh:
 // 22-106): Frechet U blocks sum D.U and U.D separately and add them, combines
@@ -86,22 +86,43 @@ __device__ __forceinline__ PQ<Pair> ptranspose(const PQ<Pair>& a, float* t, int 
   return r;
 }
 
-// Lanes in the banks (groups of 4 lanes of a row of 16) set in `Banks` take
-// the value rotated in by `Ctrl`; the others keep their own.
-template <int Ctrl, int Banks>
-__device__ __forceinline__ float dpp_take(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), Ctrl, 0xF, Banks, false));
-}
+// Left operands are held as whole rows: lane (m, I, J, q) keeps row 4I + q
+// of its matrix, all 8 entries, so the A operand of every block step is one
+// of its own registers.
+struct Q8 {
+  float v[8];
+};
+template <bool Pair>
+struct PR {
+  Q8 d;
+  Q8 u;
+};
 
-// A operands of block step K from the R layout of X: banks with J != K
-// (J is bit 0 of the bank) take the lane 4 away.
-template <int K>
-__device__ __forceinline__ Q a_operand(const Q& xr) {
-  Q r;
+// Row 4I + q of the matrix whose C layout sits in plane t: entries 4K..4K+3
+// are row q of block (I, K), read from that block's slot as plane_read does.
+__device__ __forceinline__ Q8 plane_rows(const float* t, int lane) {
+  const int b = lane >> 2, q = lane & 3;
+  Q8 r;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) r.v[k] = K == 0 ? dpp_take<kRor4, 0xA>(xr.v[k]) : dpp_take<kRor12, 0x5>(xr.v[k]);
+  for (int K = 0; K < 2; ++K)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) r.v[4 * K + k] = t[k * 64 + 4 * (((b & ~1) | K) ^ (2 * k)) + q];
   return r;
 }
+
+template <bool Pair>
+__device__ __forceinline__ PR<Pair> prows(const PQ<Pair>& c, float* t, int lane) {
+  plane_write(c.d, t, lane);
+  if constexpr (Pair) plane_write(c.u, t + 256, lane);
+  lds_order();
+  PR<Pair> r;
+  r.d = plane_rows(t, lane);
+  if constexpr (Pair) r.u = plane_rows(t + 256, lane);
+  lds_order();
+  return r;
+}
+
+__device__ __forceinline__ Q half(const Q8& x, int K) { return Q{{x.v[4 * K], x.v[4 * K + 1], x.v[4 * K + 2], x.v[4 * K + 3]}}; }
 // B operands of block step K from the C layout of Y: banks with I != K (I is
 // bit 1 of the bank) take the lane 8 away.  Both steps select between the
 // lane's own registers and one full row_ror:8 copy.
@@ -130,19 +151,19 @@ __device__ __forceinline__ Q chain(const Q& a0, const Q& b0, const Q& a1, const 
   return Q{{acc[0], acc[1], acc[2], acc[3]}};
 }
 
-// Structured (Frechet) product (D1.D2, D1.U2 + U1.D2) in C layout from X in
-// R layout and Y in C layout; the two U sums are kept separate and added last
-// (csrc/MatrixExpSmall.cuh:34-49).
+// Structured (Frechet) product (D1.D2, D1.U2 + U1.D2) in C layout from X as
+// whole rows and Y in C layout; the two U sums are kept separate and added
+// last (csrc/MatrixExpSmall.cuh:34-49).
 template <bool Pair>
-__device__ __forceinline__ PQ<Pair> pmm(const PQ<Pair>& xr, const PQ<Pair>& yc) {
-  const Q ad0 = a_operand<0>(xr.d), ad1 = a_operand<1>(xr.d);
+__device__ __forceinline__ PQ<Pair> pmm(const PR<Pair>& xr, const PQ<Pair>& yc) {
+  const Q ad0 = half(xr.d, 0), ad1 = half(xr.d, 1);
   const BPair bd = b_operands(yc.d);
   PQ<Pair> c;
   c.d = chain(ad0, bd.k0, ad1, bd.k1);
   if constexpr (Pair) {
     const BPair bu = b_operands(yc.u);
     const Q u = chain(ad0, bu.k0, ad1, bu.k1);
-    const Q v = chain(a_operand<0>(xr.u), bd.k0, a_operand<1>(xr.u), bd.k1);
+    const Q v = chain(half(xr.u, 0), bd.k0, half(xr.u, 1), bd.k1);
 #pragma unroll
     for (int r = 0; r < 4; ++r) c.u.v[r] = u.v[r] + v.v[r];
   }
@@ -201,15 +222,15 @@ __device__ __forceinline__ PQ<Pair> padd(const PQ<Pair>& a, const PQ<Pair>& b) {
 // (csrc/MatrixExpSmall.cuh:83-106): A2 = A.A, A3 = A2.A, A6 = A3.A3,
 // A9 = B1.B5 + B4, T = B2 + (B3 + A9).A9.  Result in C layout.
 template <bool Pair>
-__device__ __forceinline__ PQ<Pair> t18(const PQ<Pair>& ar, const PQ<Pair>& ac, const Q& diag, float* t,
+__device__ __forceinline__ PQ<Pair> t18(const PR<Pair>& ar, const PQ<Pair>& ac, const Q& diag, float* t,
                                         int lane) {
   const PQ<Pair> a2 = pmm<Pair>(ar, ac);
-  const PQ<Pair> a3 = pmm<Pair>(ptranspose<Pair>(a2, t, lane), ac);
-  const PQ<Pair> a6 = pmm<Pair>(ptranspose<Pair>(a3, t, lane), a3);
-  const PQ<Pair> b1r = ptranspose<Pair>(comb<0, Pair>(ac, a2, a3, a6, diag), t, lane);
+  const PQ<Pair> a3 = pmm<Pair>(prows<Pair>(a2, t, lane), ac);
+  const PQ<Pair> a6 = pmm<Pair>(prows<Pair>(a3, t, lane), a3);
+  const PR<Pair> b1r = prows<Pair>(comb<0, Pair>(ac, a2, a3, a6, diag), t, lane);
   PQ<Pair> a9 = pmm<Pair>(b1r, comb<4, Pair>(ac, a2, a3, a6, diag));
   a9 = padd<Pair>(a9, comb<3, Pair>(ac, a2, a3, a6, diag));
-  const PQ<Pair> lhsr = ptranspose<Pair>(padd<Pair>(comb<2, Pair>(ac, a2, a3, a6, diag), a9), t, lane);
+  const PR<Pair> lhsr = prows<Pair>(padd<Pair>(comb<2, Pair>(ac, a2, a3, a6, diag), a9), t, lane);
   return padd<Pair>(comb<1, Pair>(ac, a2, a3, a6, diag), pmm<Pair>(lhsr, a9));
 }
 
@@ -393,17 +414,16 @@ __global__ __launch_bounds__(64 * kOctWaves) void expm_oct_kernel(ExpmArgs args)
     if constexpr (Pair) lx.u = to_q<T>(next.g);
     if (unit + stride < units) next = load_unit(unit + stride);
 
-    // Both layouts of X (and G).
-    PQ<Pair> ar, ac;
-    {
+    // X (and G) in the C layout and as whole rows.
+    PQ<Pair> ac;
+    if constexpr (XL == kVecRows || GL == kVecRows) {
       const PQ<Pair> other = ptranspose<Pair>(lx, t, lane);
-      ar.d = XL == kVecRows ? lx.d : other.d;
       ac.d = XL == kVecRows ? other.d : lx.d;
-      if constexpr (Pair) {
-        ar.u = GL == kVecRows ? lx.u : other.u;
-        ac.u = GL == kVecRows ? other.u : lx.u;
-      }
+      if constexpr (Pair) ac.u = GL == kVecRows ? other.u : lx.u;
+    } else {
+      ac = lx;
     }
+    PR<Pair> ar = prows<Pair>(ac, t, lane);
 
     const int s = matrix_squarings<Pair>(ac, I);
     const bool bad = s < 0;
@@ -415,12 +435,13 @@ __global__ __launch_bounds__(64 * kOctWaves) void expm_oct_kernel(ExpmArgs args)
     const float scale_g = scale * args.g.sign;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      ar.d.v[r] *= scale_x;
       ac.d.v[r] *= scale_x;
-      if constexpr (Pair) {
-        ar.u.v[r] *= scale_g;
-        ac.u.v[r] *= scale_g;
-      }
+      if constexpr (Pair) ac.u.v[r] *= scale_g;
+    }
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      ar.d.v[r] *= scale_x;
+      if constexpr (Pair) ar.u.v[r] *= scale_g;
     }
 
     PQ<Pair> res = t18<Pair>(ar, ac, diag, t, lane);
@@ -429,7 +450,7 @@ __global__ __launch_bounds__(64 * kOctWaves) void expm_oct_kernel(ExpmArgs args)
     // loops while any of its matrices still needs one and each keeps its own
     // result.
     for (int it = 0; __builtin_amdgcn_ballot_w64(it < s) != 0; ++it) {
-      const PQ<Pair> sq = pmm<Pair>(ptranspose<Pair>(res, t, lane), res);
+      const PQ<Pair> sq = pmm<Pair>(prows<Pair>(res, t, lane), res);
       const bool keep = it < s;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {

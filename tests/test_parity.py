@@ -108,6 +108,24 @@ def test_small_kernels_bitwise(n, dtype, backward):
     assert ok, f"{bad} elements differ from the oracle"
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n", [3, 4])
+def test_p4_frechet_large_batch_bitwise(n, dtype):
+    """The persistent P = 4 Frechet kernel over half a million matrices: several groups
+    per wavefront (prefetch of the next group, staged stores, a partial last group) with
+    squaring counts spread over 0..7 inside every wavefront.  Each matrix must match the
+    oracle bit for bit."""
+    batch = (1 << 19) + 37
+    a, g = scaled_inputs(batch, n, dtype, seed=91 * n + DTYPES.index(dtype), low=-3.0, high=2.0)
+    x = a.cuda().mT
+    out, s = run_kernel(x, g.cuda(), AUTO)
+    exp_out, exp_s = oracle_result(x, g)
+    assert torch.equal(s.cpu(), exp_s)
+    assert int(exp_s.max()) >= 6 and int((exp_s == 0).sum()) > 0
+    ok, bad = same_values(out, exp_out)
+    assert ok, f"{bad} elements differ from the oracle"
+
+
 @pytest.mark.parametrize("n", [4, 8, 16, 32])
 def test_nonfinite_rule_matches_oracle(n):
     a = torch.zeros(5, n, n, device="cuda")

@@ -6,20 +6,22 @@
 // I = bit 3 and J = bit 2 of l, and index q = l%4 inside the block.  A
 // matrix value is held in the C (column) layout of four VGPRs,
 //   v[r] = M[4I + r][4J + q],
-// and a left operand of a product as a whole row of eight VGPRs,
-//   v[k] = M[4I + q][k],  k = 0..7.
+// the left operand of a product as a whole row of eight VGPRs,
+//   v[k] = M[4I + q][k],  k = 0..7,
+// and the right operand as a whole column of eight VGPRs,
+//   v[k] = M[k][4J + q].
 // The 4x4x1 MFMA multiplies 16 independent 4 x 4 blocks per instruction
 // (block b's lanes supply A[i][0] from lane 4b+i and B[0][j] from lane 4b+j;
 // D[i][j] lands in lane 4b+j, VGPR i), so output block (I, J) of X.Y is
 //   sum over K = 0, 1 and k = 0..3 of  X_IK[:, k] (x) Y_KJ[k, :].
-// Its A operand is row q of X block (I, K), entries 4K..4K+3 of the lane's
-// own row registers; its B operand is column q of Y block (K, J): own C
-// registers when K == I, else those of the lane 8 away, a select between the
-// lane's own registers and one row_ror 8 DPP copy shared by both steps.
-// Steps run K = 0, 1 in turn -- the products accumulate k = 0..7 in the
-// reference's order from +0, each step one exact FMA (csrc/MatrixExpSmall.cuh:
-// 31-33).  Rows are formed from the C layout through the wavefront's LDS plane
-// (one 16-byte write and eight reads per lane).
+// Its A operand is row q of X block (I, K) and its B operand column q of Y
+// block (K, J): entries 4K..4K+3 of the lane's own row and column registers,
+// so no step moves data between lanes.  Steps run K = 0, 1 in turn -- the
+// products accumulate k = 0..7 in the reference's order from +0, each step
+// one exact FMA (csrc/MatrixExpSmall.cuh:31-33).  Rows and columns are formed
+// from the C layout through the wavefront's LDS plane: one 16-byte write per
+// lane, then eight 4-byte reads for a row and two 16-byte reads for a
+// column.
 //
 // Arithmetic is the reference's, element by element (csrc/MatrixExpSmall.cuh:
 // 22-106): Frechet U blocks sum D.U and U.D separately and add them, combines
@@ -122,48 +124,64 @@ __device__ __forceinline__ PR<Pair> prows(const PQ<Pair>& c, float* t, int lane)
   return r;
 }
 
-__device__ __forceinline__ Q half(const Q8& x, int K) { return Q{{x.v[4 * K], x.v[4 * K + 1], x.v[4 * K + 2], x.v[4 * K + 3]}}; }
-// B operands of block step K from the C layout of Y: banks with I != K (I is
-// bit 1 of the bank) take the lane 8 away.  Both steps select between the
-// lane's own registers and one full row_ror:8 copy.
-struct BPair {
-  Q k0, k1;
-};
-__device__ __forceinline__ BPair b_operands(const Q& yc) {
-  const bool upper = (__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) & 8) != 0;
-  BPair r;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const float far = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(yc.v[k]), kRor8, 0xF, 0xF, false));
-    r.k0.v[k] = upper ? far : yc.v[k];
-    r.k1.v[k] = upper ? yc.v[k] : far;
-  }
+// Whole column 4J + q of the matrix whose C layout sits in plane t: entries
+// 0..3 are column q of block (0, J), entries 4..7 column q of block (1, J),
+// each one 16-byte chunk of plane row q (slots as plane_write puts them).
+__device__ __forceinline__ Q8 plane_cols(const float* t, int lane) {
+  const int b = lane >> 2, q = lane & 3;
+  const float* row = t + q * 64;
+  const float4 lo = *reinterpret_cast<const float4*>(row + 4 * ((b & ~2) ^ (2 * q)));
+  const float4 hi = *reinterpret_cast<const float4*>(row + 4 * ((b | 2) ^ (2 * q)));
+  return Q8{{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w}};
+}
+
+template <bool Pair>
+__device__ __forceinline__ PR<Pair> pcols(const PQ<Pair>& c, float* t, int lane) {
+  plane_write(c.d, t, lane);
+  if constexpr (Pair) plane_write(c.u, t + 256, lane);
+  lds_order();
+  PR<Pair> r;
+  r.d = plane_cols(t, lane);
+  if constexpr (Pair) r.u = plane_cols(t + 256, lane);
+  lds_order();
   return r;
 }
 
-// One block product chain: k = 0..7 (K = 0 block first), from +0.
-__device__ __forceinline__ Q chain(const Q& a0, const Q& b0, const Q& a1, const Q& b1) {
+// Rows and columns of one value through a single plane write.
+template <bool Pair>
+__device__ __forceinline__ void prowcols(const PQ<Pair>& c, float* t, int lane, PR<Pair>& rows, PR<Pair>& cols) {
+  plane_write(c.d, t, lane);
+  if constexpr (Pair) plane_write(c.u, t + 256, lane);
+  lds_order();
+  rows.d = plane_rows(t, lane);
+  cols.d = plane_cols(t, lane);
+  if constexpr (Pair) {
+    rows.u = plane_rows(t + 256, lane);
+    cols.u = plane_cols(t + 256, lane);
+  }
+  lds_order();
+}
+
+// One block product chain: k = 0..7 (K = 0 block first), from +0.  Step
+// (K, k) takes A = row q of X block (I, K), entry k, and B = column q of Y
+// block (K, J), entry k: entries 4K + k of the lane's row and column.
+__device__ __forceinline__ Q chain(const Q8& xr, const Q8& yc) {
   v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int k = 0; k < 4; ++k) acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a0.v[k], b0.v[k], acc, 0, 0, 0);
-#pragma unroll
-  for (int k = 0; k < 4; ++k) acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a1.v[k], b1.v[k], acc, 0, 0, 0);
+  for (int k = 0; k < 8; ++k) acc = __builtin_amdgcn_mfma_f32_4x4x1f32(xr.v[k], yc.v[k], acc, 0, 0, 0);
   return Q{{acc[0], acc[1], acc[2], acc[3]}};
 }
 
 // Structured (Frechet) product (D1.D2, D1.U2 + U1.D2) in C layout from X as
-// whole rows and Y in C layout; the two U sums are kept separate and added
-// last (csrc/MatrixExpSmall.cuh:34-49).
+// whole rows and Y as whole columns; the two U sums are kept separate and
+// added last (csrc/MatrixExpSmall.cuh:34-49).
 template <bool Pair>
-__device__ __forceinline__ PQ<Pair> pmm(const PR<Pair>& xr, const PQ<Pair>& yc) {
-  const Q ad0 = half(xr.d, 0), ad1 = half(xr.d, 1);
-  const BPair bd = b_operands(yc.d);
+__device__ __forceinline__ PQ<Pair> pmm(const PR<Pair>& xr, const PR<Pair>& yc) {
   PQ<Pair> c;
-  c.d = chain(ad0, bd.k0, ad1, bd.k1);
+  c.d = chain(xr.d, yc.d);
   if constexpr (Pair) {
-    const BPair bu = b_operands(yc.u);
-    const Q u = chain(ad0, bu.k0, ad1, bu.k1);
-    const Q v = chain(half(xr.u, 0), bd.k0, half(xr.u, 1), bd.k1);
+    const Q u = chain(xr.d, yc.u);
+    const Q v = chain(xr.u, yc.d);
 #pragma unroll
     for (int r = 0; r < 4; ++r) c.u.v[r] = u.v[r] + v.v[r];
   }
@@ -222,16 +240,18 @@ __device__ __forceinline__ PQ<Pair> padd(const PQ<Pair>& a, const PQ<Pair>& b) {
 // (csrc/MatrixExpSmall.cuh:83-106): A2 = A.A, A3 = A2.A, A6 = A3.A3,
 // A9 = B1.B5 + B4, T = B2 + (B3 + A9).A9.  Result in C layout.
 template <bool Pair>
-__device__ __forceinline__ PQ<Pair> t18(const PR<Pair>& ar, const PQ<Pair>& ac, const Q& diag, float* t,
-                                        int lane) {
-  const PQ<Pair> a2 = pmm<Pair>(ar, ac);
-  const PQ<Pair> a3 = pmm<Pair>(prows<Pair>(a2, t, lane), ac);
-  const PQ<Pair> a6 = pmm<Pair>(prows<Pair>(a3, t, lane), a3);
+__device__ __forceinline__ PQ<Pair> t18(const PR<Pair>& ar, const PR<Pair>& acol, const PQ<Pair>& ac,
+                                        const Q& diag, float* t, int lane) {
+  const PQ<Pair> a2 = pmm<Pair>(ar, acol);
+  const PQ<Pair> a3 = pmm<Pair>(prows<Pair>(a2, t, lane), acol);
+  PR<Pair> a3r, a3c;
+  prowcols<Pair>(a3, t, lane, a3r, a3c);
+  const PQ<Pair> a6 = pmm<Pair>(a3r, a3c);
   const PR<Pair> b1r = prows<Pair>(comb<0, Pair>(ac, a2, a3, a6, diag), t, lane);
-  PQ<Pair> a9 = pmm<Pair>(b1r, comb<4, Pair>(ac, a2, a3, a6, diag));
+  PQ<Pair> a9 = pmm<Pair>(b1r, pcols<Pair>(comb<4, Pair>(ac, a2, a3, a6, diag), t, lane));
   a9 = padd<Pair>(a9, comb<3, Pair>(ac, a2, a3, a6, diag));
   const PR<Pair> lhsr = prows<Pair>(padd<Pair>(comb<2, Pair>(ac, a2, a3, a6, diag), a9), t, lane);
-  return padd<Pair>(comb<1, Pair>(ac, a2, a3, a6, diag), pmm<Pair>(lhsr, a9));
+  return padd<Pair>(comb<1, Pair>(ac, a2, a3, a6, diag), pmm<Pair>(lhsr, pcols<Pair>(a9, t, lane)));
 }
 
 // ---- norm ---------------------------------------------------------------------
@@ -423,7 +443,8 @@ __global__ __launch_bounds__(64 * kOctWaves) void expm_oct_kernel(ExpmArgs args)
     } else {
       ac = lx;
     }
-    PR<Pair> ar = prows<Pair>(ac, t, lane);
+    PR<Pair> ar, acol;
+    prowcols<Pair>(ac, t, lane, ar, acol);
 
     const int s = matrix_squarings<Pair>(ac, I);
     const bool bad = s < 0;
@@ -441,16 +462,22 @@ __global__ __launch_bounds__(64 * kOctWaves) void expm_oct_kernel(ExpmArgs args)
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
       ar.d.v[r] *= scale_x;
-      if constexpr (Pair) ar.u.v[r] *= scale_g;
+      acol.d.v[r] *= scale_x;
+      if constexpr (Pair) {
+        ar.u.v[r] *= scale_g;
+        acol.u.v[r] *= scale_g;
+      }
     }
 
-    PQ<Pair> res = t18<Pair>(ar, ac, diag, t, lane);
+    PQ<Pair> res = t18<Pair>(ar, acol, ac, diag, t, lane);
 
     // s squarings per matrix (csrc/MatrixExpSmall.cuh:168); the wavefront
     // loops while any of its matrices still needs one and each keeps its own
     // result.
     for (int it = 0; __builtin_amdgcn_ballot_w64(it < s) != 0; ++it) {
-      const PQ<Pair> sq = pmm<Pair>(prows<Pair>(res, t, lane), res);
+      PR<Pair> rr, rc;
+      prowcols<Pair>(res, t, lane, rr, rc);
+      const PQ<Pair> sq = pmm<Pair>(rr, rc);
       const bool keep = it < s;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {

@@ -395,9 +395,12 @@ struct UnitRaw {
 // ---- kernel -----------------------------------------------------------------
 
 // Persistent kernel: each wavefront walks 4-matrix units with a grid stride
-// and issues the next unit's loads before computing the current one.
+// and issues the next unit's loads before computing the current one.  Four
+// wavefronts per SIMD (at most 128 VGPRs): the element-wise Frechet variant
+// (n < 8) would take 133 and run three; held to 128 it spills 16-32 bytes and
+// is 6% faster at [262144, 6, 6].
 template <typename T, bool Pair, int XL, int GL>
-__global__ __launch_bounds__(64 * kOctWaves) void expm_oct_kernel(ExpmArgs args) {
+__global__ __launch_bounds__(64 * kOctWaves) __attribute__((amdgpu_waves_per_eu(4, 8))) void expm_oct_kernel(ExpmArgs args) {
   using S = typename T::storage;
   __shared__ float lds[kOctWaves][kOctLds];
   const int lane = threadIdx.x & 63;

@@ -108,6 +108,44 @@ def test_small_kernels_bitwise(n, dtype, backward):
     assert ok, f"{bad} elements differ from the oracle"
 
 
+def _laid_out(m, layout):
+    """The same logical [B, n, n] values stored row-major ("rows": every row one aligned
+    vector), column-major ("cols": a transposed view) or with a padded row stride that no
+    vector class accepts ("none")."""
+    if layout == "rows":
+        return m.contiguous()
+    if layout == "cols":
+        return m.mT.contiguous().mT
+    b, n, _ = m.shape
+    padded = torch.zeros(b, n, n + 1, dtype=m.dtype, device=m.device)
+    padded[:, :, :n] = m
+    return padded[:, :, :n]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n", [4, 8])
+def test_small_kernels_bitwise_all_layouts(n, dtype):
+    """Every load path of the P = 4 and P = 8 kernels (row vectors, column vectors,
+    element-wise; X and G classified independently, dense or not) gives the oracle's
+    values bit for bit, forward and Frechet, over a batch with a partial last group."""
+    a, g = scaled_inputs(300, n, dtype, seed=577 * n + DTYPES.index(dtype))
+    a, g = a.cuda(), g.cuda()
+    for xl in ("rows", "cols", "none"):
+        x = _laid_out(a, xl)
+        out, s = run_kernel(x, None, AUTO)
+        exp_out, exp_s = oracle_result(x, None)
+        assert torch.equal(s.cpu(), exp_s), xl
+        ok, bad = same_values(out, exp_out)
+        assert ok, f"forward, x {xl}: {bad} elements differ from the oracle"
+        for gl in ("rows", "cols", "none"):
+            d = _laid_out(g, gl)
+            out, s = run_kernel(x, d, AUTO)
+            exp_out, exp_s = oracle_result(x, d)
+            assert torch.equal(s.cpu(), exp_s), (xl, gl)
+            ok, bad = same_values(out, exp_out)
+            assert ok, f"Frechet, x {xl}, g {gl}: {bad} elements differ from the oracle"
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("n", [3, 4])
 def test_p4_frechet_large_batch_bitwise(n, dtype):

@@ -3,23 +3,38 @@
 Headline (``value``): BASELINE config 2 -- [1048576, 4, 4] FP32, entries N(0, 0.25^2),
 upstream gradient N(0, 1); one step = ``fh.matrix_exp`` forward plus
 ``torch.autograd.grad`` backward over the whole batch, inputs resident in HBM.
-Metric: matrices per second of forward + backward.
+Metric: matrices per second of forward + backward.  The K timed steps are split
+into >= 5 trials, each bracketed by a device synchronisation and timed with HIP
+events on the stream the kernels run on; ``ms_per_step`` is the median over the
+trials of the per-step time (every trial's time is kept in ``trials_ms``).
 
 Also reported in the same JSON line:
-* ``roofline`` -- the dominant kernel of that step (the P = 4 Frechet kernel),
-  algorithmic bytes per launch / its mean launch time from HIP events on the
-  stream it runs on, against MI355X's 8 TB/s;
-* ``cpu_baseline`` -- the CPU restatement (oracle/, scalar C, one thread) over
-  the same workload; ``cpu_native_torch`` -- native torch.linalg.matrix_exp +
-  autograd on the host cores (the reference's own CPU path), on a sample;
+* ``roofline`` -- the dominant kernel of that step (the P = 4 Frechet kernel):
+  algorithmic bytes per launch / its median launch time (HIP events around
+  back-to-back launches, same trial split) against MI355X's 8 TB/s;
+* ``cold_step`` -- the same step cycling through 4 input/gradient sets
+  (512 MiB of inputs, more than the 256 MB Infinity Cache), so that no launch
+  finds its operands in the last-level cache;
+* ``cpu_baseline`` -- the reference's CPU path (its ``matrix_exp`` falls through
+  to native ``torch.linalg.matrix_exp`` on CPU tensors, backward by autograd)
+  over ALL config-2 matrices on the host threads this process may use;
+  ``cpu_oracle_port`` -- the C restatement (oracle/, one thread) over the same
+  workload, whose results feed ``parity``;
+* ``parity`` -- per config, over every matrix: squaring counts against the
+  restatement, bitwise mismatches, strict north-star failures of the kernels
+  and of the restatement, the kernels' error relative to the restatement's
+  (tests/fullsize.py), all computed after the timed region;
 * ``configs`` -- configs 3-5 (BF16 N=4 sweep, strided FP32 N=16, FP16 N=32 and
-  the same shape in FP32) with their own rooflines (HBM for N=4, FP32 MFMA for
-  N>=16, where the flop count uses each matrix's own squaring count);
+  the same shape in FP32) plus ``p8`` / ``c2s8`` with their own rooflines (HBM
+  bytes at 8 TB/s, product flops from each matrix's own squaring count at the
+  FP32 matrix peak);
 * ``reference_table`` -- the reference's own benchmark (N = 4, 8, 16, 32 at
   B = 65,536 FP32, wall time per direct-API call) beside its published A100
-  figures; ``small_batch_latency`` -- B = 1 wall time per call.
+  figures; ``stock_gpu`` -- native torch.linalg.matrix_exp + autograd on this
+  GPU in the same sweep; ``small_batch_latency`` -- B = 1 wall time per call.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--only c2]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--trials T] [--skip-cpu]
+                       [--only c2,...] [--extras] [--sweep]
 """
 
 from __future__ import annotations
@@ -29,6 +44,7 @@ import hashlib
 import json
 import os
 import statistics
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -40,6 +56,7 @@ for _p in (str(ROOT / "flash-hyperconnections_amd"), str(ROOT)):
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 MFMA_F32_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix
+VALU_F32_UNPACKED_TFLOPS = 78.6  # 256 CUs x 4 SIMDs x 16 lanes x 2 flops x 2.4 GHz (packed FP32 is not used)
 METRIC = "matrices/sec fwd+bwd (N=4 B=2^20, N=32 B=32768); % HBM/MFMA roofline"
 
 
@@ -101,23 +118,42 @@ def sha256(t) -> str:
     return hashlib.sha256(t.detach().contiguous().cpu().view(torch.uint8).numpy().tobytes()).hexdigest()
 
 
-def time_loop(torch, fn, iters: int, warmup: int) -> float:
-    """Mean ms per call of fn(), HIP events on the current stream (where the kernels launch)."""
+def split_trials(total: int, trials: int) -> list[int]:
+    """Sizes of `trials` consecutive trials covering exactly `total` steps (>= 1 each)."""
+    trials = max(1, min(trials, total))
+    base, extra = divmod(total, trials)
+    return [base + (1 if i < extra else 0) for i in range(trials)]
+
+
+def time_trials(torch, fn, steps: int, warmup: int, trials: int) -> dict:
+    """`warmup` untimed calls, then exactly `steps` timed calls split into trials; each trial is
+    bracketed by torch.cuda.synchronize() and timed with HIP events on the current stream (the one
+    the kernels launch on).  Returns the median and every trial's ms per call."""
     stream = torch.cuda.current_stream()
     for _ in range(warmup):
         fn()
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(iters):
-        fn()
-    end.record(stream)
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / iters
+    per_call = []
+    for size in split_trials(steps, trials):
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(size):
+            fn()
+        end.record(stream)
+        torch.cuda.synchronize()
+        per_call.append(start.elapsed_time(end) / size)
+    return {"median_ms": statistics.median(per_call), "trials_ms": per_call,
+            "mean_ms": sum(p * s for p, s in zip(per_call, split_trials(steps, trials))) / steps}
 
 
-def measure_config(name: str, torch, fh, steps: int, warmup: int, device) -> dict:
+def roofline_times(nbytes: float, nflops: float, compute_peak_tflops: float):
+    """(bound, seconds) of max(bytes / HBM peak, flops / compute peak)."""
+    t_hbm, t_cmp = nbytes / (HBM_PEAK_GBS * 1e9), nflops / (compute_peak_tflops * 1e12)
+    return ("hbm", t_hbm) if t_hbm >= t_cmp else ("mfma", t_cmp)
+
+
+def measure_config(name: str, torch, fh, steps: int, warmup: int, trials: int, device, keep: bool) -> tuple[dict, dict]:
     x, g, layout = make_inputs(name, torch, device)
     b, n = x.shape[0], x.shape[-1]
     e = x.element_size()
@@ -130,9 +166,10 @@ def measure_config(name: str, torch, fh, steps: int, warmup: int, device) -> dic
     fwd = torch.ops.flash_hypercons._matrix_exp
     bwd = torch.ops.flash_hypercons._frechet
     xt = x.detach().mT
-    ms_step = time_loop(torch, step, steps, warmup)
-    ms_fwd = time_loop(torch, lambda: fwd(x), steps, warmup)
-    ms_bwd = time_loop(torch, lambda: bwd(xt, g), steps, warmup)
+    t_step = time_trials(torch, step, steps, warmup, trials)
+    t_fwd = time_trials(torch, lambda: fwd(x), steps, warmup, trials)
+    t_bwd = time_trials(torch, lambda: bwd(xt, g), steps, warmup, trials)
+    ms_step, ms_fwd, ms_bwd = t_step["median_ms"], t_fwd["median_ms"], t_bwd["median_ms"]
 
     # Graph-captured step (launch overhead removed): same kernels, replayed.
     ms_graph = None
@@ -146,7 +183,7 @@ def measure_config(name: str, torch, fh, steps: int, warmup: int, device) -> dic
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             step()
-        ms_graph = time_loop(torch, graph.replay, steps, 2)
+        ms_graph = time_trials(torch, graph.replay, steps, 2, trials)["median_ms"]
     except Exception as exc:  # pragma: no cover - reported, not fatal
         log(f"[bench] graph capture of {name} failed: {exc}")
 
@@ -158,23 +195,22 @@ def measure_config(name: str, torch, fh, steps: int, warmup: int, device) -> dic
     bytes_bwd = b * n * n * 3 * e
     flops_fwd = float(((5 + s_f) * 2 * n**3).sum())
     flops_bwd = float(((5 + s_b) * 3 * 2 * n**3).sum())
-    # Roofline time = max(bytes / HBM peak, flops / FP32 matrix peak), per kernel and per step.
-    def ideal(nbytes, nflops):
-        t_hbm, t_mfma = nbytes / (HBM_PEAK_GBS * 1e9), nflops / (MFMA_F32_PEAK_TFLOPS * 1e12)
-        return ("hbm", t_hbm) if t_hbm >= t_mfma else ("mfma", t_mfma)
-
-    bound, t_ideal = ideal(bytes_fwd + bytes_bwd, flops_fwd + flops_bwd)
-    bound_fwd, t_fwd = ideal(bytes_fwd, flops_fwd)
-    bound_bwd, t_bwd = ideal(bytes_bwd, flops_bwd)
+    peak = MFMA_F32_PEAK_TFLOPS
+    bound, t_ideal = roofline_times(bytes_fwd + bytes_bwd, flops_fwd + flops_bwd, peak)
+    bound_fwd, t_f = roofline_times(bytes_fwd, flops_fwd, peak)
+    bound_bwd, t_b = roofline_times(bytes_bwd, flops_bwd, peak)
     out = {
         "shape": [b, n, n],
         "dtype": str(x.dtype).replace("torch.", ""),
         "layout": layout,
         "matrices_per_s_fwd_bwd": b / (ms_step * 1e-3),
         "ms_step": ms_step,
+        "ms_step_trials": t_step["trials_ms"],
         "ms_step_graph": ms_graph,
         "ms_fwd_kernel": ms_fwd,
         "ms_bwd_kernel": ms_bwd,
+        "ms_fwd_trials": t_fwd["trials_ms"],
+        "ms_bwd_trials": t_bwd["trials_ms"],
         "mean_s_fwd": float(s_f.mean()),
         "mean_s_bwd": float(s_b.mean()),
         "bound": bound,
@@ -183,19 +219,54 @@ def measure_config(name: str, torch, fh, steps: int, warmup: int, device) -> dic
             "bound": bound_fwd,
             "achieved_gbs": bytes_fwd / (ms_fwd * 1e-3) / 1e9,
             "achieved_tflops": flops_fwd / (ms_fwd * 1e-3) / 1e12,
-            "frac": t_fwd / (ms_fwd * 1e-3),
+            "frac": t_f / (ms_fwd * 1e-3),
         },
         "bwd_kernel": {
             "bound": bound_bwd,
             "achieved_gbs": bytes_bwd / (ms_bwd * 1e-3) / 1e9,
             "achieved_tflops": flops_bwd / (ms_bwd * 1e-3) / 1e12,
-            "frac": t_bwd / (ms_bwd * 1e-3),
+            "frac": t_b / (ms_bwd * 1e-3),
         },
         "input_sha256": sha256(x)[:16],
         "grad_sha256": sha256(g)[:16],
     }
-    del xin, x, g, xt
-    return out
+    if n <= 4:
+        # P = 4 runs on the (unpacked) FP32 VALU: report against that peak as well.
+        _, t_valu = roofline_times(bytes_fwd + bytes_bwd, flops_fwd + flops_bwd, VALU_F32_UNPACKED_TFLOPS)
+        out["roofline_frac_step_unpacked_valu_peak"] = t_valu / (ms_step * 1e-3)
+    kept = {}
+    if keep:
+        y = fh.matrix_exp(xin)
+        (grad,) = torch.autograd.grad(y, xin, g)
+        kept = {"x": x.detach(), "g": g, "y": y.detach(), "grad": grad}
+    del xin
+    return out, kept
+
+
+def cold_step(torch, fh, steps: int, warmup: int, trials: int, device, sets: int = 4) -> dict:
+    """Config 2's step cycling through `sets` distinct input/gradient sets (each 128 MiB), so the
+    working set of consecutive steps exceeds the 256 MB last-level cache."""
+    pairs = []
+    for k in range(sets):
+        if k == 0:
+            x, g, _ = make_inputs("c2", torch, device)
+        else:
+            gen = torch.Generator(device=device).manual_seed(1000 + k)
+            x = torch.randn(1 << 20, 4, 4, device=device, generator=gen) * 0.25
+            g = torch.randn(1 << 20, 4, 4, device=device, generator=gen)
+        pairs.append((x.detach().requires_grad_(), g))
+    state = {"i": 0}
+
+    def step():
+        x, g = pairs[state["i"] % sets]
+        state["i"] += 1
+        y = fh.matrix_exp(x)
+        return torch.autograd.grad(y, x, g)[0]
+
+    t = time_trials(torch, step, steps, warmup, trials)
+    b = pairs[0][0].shape[0]
+    return {"sets": sets, "input_mib": sets * 2 * b * 16 * 4 / 2**20, "ms_step": t["median_ms"],
+            "ms_step_trials": t["trials_ms"], "matrices_per_s_fwd_bwd": b / (t["median_ms"] * 1e-3)}
 
 
 def profiled_traffic(key: str):
@@ -210,38 +281,50 @@ def profiled_traffic(key: str):
     return None
 
 
-def cpu_oracle_baseline(torch) -> dict:
-    """The CPU restatement (scalar C, 1 thread) over the full config-2 workload."""
+def _cpu_model() -> tuple[str, int | None]:
+    """lscpu model name and physical core count of the whole host (sockets x cores per socket)."""
+    model, cores, sockets = "", None, None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            val = val.strip()
+            if key.strip() == "Model name":
+                model = val
+            elif key.strip() == "Core(s) per socket":
+                cores = int(val)
+            elif key.strip() == "Socket(s)":
+                sockets = int(val)
+    except (OSError, ValueError, subprocess.SubprocessError):
+        pass
+    return model, (cores * sockets if cores and sockets else None)
+
+
+def cpu_leg(torch, kept: dict) -> dict:
+    """The CPU side of the run, after every GPU timing: the reference's CPU path timed over all of
+    config 2, the C restatement timed over the same workload, and the parity block built from the
+    restatement's results (the restatement is the checker here, never the thing measured on the
+    GPU)."""
     import numpy as np
 
     import oracle
+    from tests.fullsize import check, direction_parity
 
+    try:
+        threads = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        threads = os.cpu_count() or 1
+    threads = max(1, min(threads, 16))
+    model, physical = _cpu_model()
+    result = {}
+
+    # 1. The reference's CPU path: native matrix_exp + autograd on every config-2 matrix.
     x, g, _ = make_inputs("c2", torch, "cpu")
-    xf = oracle.tensor_to_f32(x)
-    gf = oracle.tensor_to_f32(g)
-    xt = np.ascontiguousarray(xf.transpose(0, 2, 1))
-    t0 = time.perf_counter()
-    oracle.matrix_exp_f32(xf)
-    oracle.matrix_exp_f32(xt, gf)
-    dt = time.perf_counter() - t0
-    return {
-        "value": x.shape[0] / dt,
-        "unit": "matrices/s",
-        "cores": 1,
-        "kind": "port",
-        "sample": f"all {x.shape[0]} config-2 matrices, forward + Frechet backward, oracle/fh_oracle.c "
-        f"(scalar C restatement, one thread), {dt:.2f} s",
-    }
-
-
-def cpu_native_torch(torch, sample: int = 1 << 18) -> dict:
-    """Native torch.linalg.matrix_exp + autograd on host cores (the reference's CPU path)."""
-    x, g, _ = make_inputs("c2", torch, "cpu")
-    x = x[:sample].clone().requires_grad_()
-    g = g[:sample].clone()
-    threads = torch.get_num_threads()
-    y = torch.linalg.matrix_exp(x[:1024])  # warm
-    torch.autograd.grad(y.sum(), x)
+    prev_threads = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    xr = x.clone().requires_grad_()
+    y = torch.linalg.matrix_exp(xr)  # warm-up call, full batch
+    torch.autograd.grad(y, xr, g)
     times, fwd_times = [], []
     for _ in range(3):
         t0 = time.perf_counter()
@@ -249,28 +332,57 @@ def cpu_native_torch(torch, sample: int = 1 << 18) -> dict:
             torch.linalg.matrix_exp(x)
         fwd_times.append(time.perf_counter() - t0)
         t0 = time.perf_counter()
-        y = torch.linalg.matrix_exp(x)
-        torch.autograd.grad(y, x, g)
+        y = torch.linalg.matrix_exp(xr)
+        torch.autograd.grad(y, xr, g)
         times.append(time.perf_counter() - t0)
     dt = statistics.median(times)
-    model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {
-        "value": sample / dt,
-        "forward_value": sample / statistics.median(fwd_times),
+    result["cpu_baseline"] = {
+        "value": x.shape[0] / dt,
         "unit": "matrices/s",
-        "cores": threads,
+        "cores": torch.get_num_threads(),
+        "kind": "reference",
+        "sample": f"all {x.shape[0]} config-2 matrices: native torch.linalg.matrix_exp + torch.autograd.grad (the "
+        f"reference's matrix_exp falls through to these on CPU tensors), 1 warm-up call, median of 3 trials "
+        f"({dt:.2f} s per trial); forward alone {statistics.median(fwd_times):.3f} s",
+        "forward_value": x.shape[0] / statistics.median(fwd_times),
+        "trials_s": times,
+        "torch_threads": torch.get_num_threads(),
         "cpu_count": os.cpu_count(),
+        "affinity_cpus": threads,
+        "physical_cores_host": physical,
         "cpu_model": model,
-        "sample": f"first {sample} config-2 matrices, torch.linalg.matrix_exp + autograd.grad "
-        f"(value) and forward alone (forward_value), median of 3",
     }
+    torch.set_num_threads(prev_threads)
+    del xr, y
+
+    # 2. The C restatement, one thread, same workload (forward + Frechet of x^T).
+    xf = oracle.tensor_to_f32(x)
+    gf = oracle.tensor_to_f32(g)
+    xt = np.ascontiguousarray(xf.transpose(0, 2, 1))
+    t0 = time.perf_counter()
+    oracle.matrix_exp_f32(xf)
+    oracle.matrix_exp_f32(xt, gf)
+    dt = time.perf_counter() - t0
+    result["cpu_oracle_port"] = {
+        "value": x.shape[0] / dt, "unit": "matrices/s", "cores": 1, "kind": "port",
+        "sample": f"all {x.shape[0]} config-2 matrices, forward + Frechet backward, oracle/fh_oracle.c (scalar C "
+        f"restatement, one thread), {dt:.2f} s",
+    }
+
+    # 3. Parity over every matrix of every measured config.
+    parity = {}
+    for name, k in kept.items():
+        t0 = time.perf_counter()
+        parity[name] = {"forward": direction_parity(k["x"], None, k["y"], threads=threads),
+                        "backward": direction_parity(k["x"].mT, k["g"], k["grad"], threads=threads)}
+        log(f"[bench] parity {name} ({time.perf_counter() - t0:.1f} s): {json.dumps(parity[name])}")
+    failures = {f"{name}.{d}": why for name, rep in parity.items() for d, r in rep.items()
+                if (why := check(r, kept[name]["x"].shape[-1]))}
+    result["parity"] = {"pass": not failures, "failures": failures, "configs": parity,
+                        "rule": "tests/fullsize.py check(): s == oracle for every matrix; n <= 8 bit-identical "
+                        "to the oracle; strict north-star failures <= the oracle's; FP32 mean error <= 1.05x "
+                        "the oracle's; per-matrix excess over the oracle's error under a sanity cap"}
+    return result
 
 
 def small_batch_latency(torch, fh, device, iters: int = 400) -> dict:
@@ -311,42 +423,69 @@ REFERENCE_A100_US = {
 }
 
 
-def reference_table(torch, fh, device, batch: int = 65536, warmup: int = 5, repeat: int = 10, trials: int = 3) -> dict:
+def reference_table(torch, fh, device, sizes=(4, 8, 16, 32), batches=(65536,), dtypes=("f32",), warmup: int = 5,
+                    repeat: int = 10, trials: int = 3) -> dict:
     """The reference's own benchmark on this GPU (its benchmarks/matrix_exp.py:75-105 method):
-    seeded inputs randn*0.1 and grads randn*0.2, FP32, B = 65,536; per mode, warmup calls, then
-    trials of back-to-back direct-API calls with synchronization at trial boundaries only; median
-    of the per-call trial means.  Wall time includes Python selection, allocation and autograd."""
+    seeded inputs randn*0.1 and grads randn*0.2; per (n, B, dtype, mode) and per implementation
+    (this operator, and native torch.linalg.matrix_exp on the same GPU -- the reference's "stock"
+    column, with FP16/BF16 promoted to FP32 and cast back as its benchmark does), warmup calls,
+    then trials of back-to-back direct-API calls with synchronisation at trial boundaries only; the
+    implementations alternate order per trial; median of the per-call trial means.  Wall time
+    includes Python selection, allocation and autograd."""
+    dt_map = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
     rows = []
-    for n in (4, 8, 16, 32):
-        seed = 9041 + n * 1000003 + batch * 3
-        torch.manual_seed(seed)
-        a = torch.randn(batch, n, n, device=device) * 0.1
-        g = torch.randn_like(a) * 0.2
-        for mode in ("forward", "forward_backward"):
-            x = a.detach().requires_grad_(mode == "forward_backward")
 
-            def call(x=x, mode=mode):
-                y = fh.matrix_exp(x)
-                if mode == "forward_backward":
-                    return torch.autograd.grad(y, x, g)[0]
-                return y
+    def native(x):
+        if x.dtype in (torch.float16, torch.bfloat16):
+            return torch.linalg.matrix_exp(x.float()).to(x.dtype)
+        return torch.linalg.matrix_exp(x)
 
-            for _ in range(warmup):
-                call()
-            times = []
-            for _ in range(trials):
-                torch.cuda.synchronize()
-                t0 = time.perf_counter()
-                for _ in range(repeat):
-                    call()
-                torch.cuda.synchronize()
-                times.append((time.perf_counter() - t0) * 1e6 / repeat)
-            us = statistics.median(times)
-            ref = REFERENCE_A100_US[(n, mode)]
-            rows.append({"n": n, "mode": mode, "median_us": us, "matrices_per_s": batch / us * 1e6,
-                         "reference_a100_us": ref, "reference_time_over_ours": ref / us})
-    return {"batch": batch, "dtype": "f32", "method": f"{warmup} warmup, {trials} trials x {repeat} calls, median",
-            "reference_source": "reference VALIDATION.md:84-95 (A100 80GB PCIe)", "rows": rows}
+    for dname in dtypes:
+        dtype = dt_map[dname]
+        for batch in batches:
+            for n in sizes:
+                seed = 9041 + n * 1000003 + batch * 3
+                torch.manual_seed(seed)
+                a = (torch.randn(batch, n, n, device=device) * 0.1).to(dtype)
+                g = (torch.randn(batch, n, n, device=device) * 0.2).to(dtype)
+                for mode in ("forward", "forward_backward"):
+                    x = a.detach().requires_grad_(mode == "forward_backward")
+                    impls = {"flash_hypercons": fh.matrix_exp, "stock": native}
+
+                    def call(fn, x=x, mode=mode, g=g):
+                        y = fn(x)
+                        if mode == "forward_backward":
+                            return torch.autograd.grad(y, x, g)[0]
+                        return y
+
+                    times = {k: [] for k in impls}
+                    for k, fn in impls.items():
+                        for _ in range(warmup):
+                            call(fn)
+                    order = list(impls)
+                    for t in range(trials):
+                        for k in (order if t % 2 == 0 else order[::-1]):
+                            torch.cuda.synchronize()
+                            t0 = time.perf_counter()
+                            for _ in range(repeat):
+                                call(impls[k])
+                            torch.cuda.synchronize()
+                            times[k].append((time.perf_counter() - t0) * 1e6 / repeat)
+                    us = statistics.median(times["flash_hypercons"])
+                    stock = statistics.median(times["stock"])
+                    row = {"n": n, "batch": batch, "dtype": dname, "mode": mode, "median_us": us,
+                           "matrices_per_s": batch / us * 1e6, "stock_gpu_us": stock, "speedup_vs_stock": stock / us,
+                           "trials_us": times["flash_hypercons"], "stock_trials_us": times["stock"]}
+                    ref = REFERENCE_A100_US.get((n, mode)) if (dname == "f32" and batch == 65536) else None
+                    if ref is not None:
+                        row["reference_a100_us"] = ref
+                        row["reference_time_over_ours"] = ref / us
+                    rows.append(row)
+                del a, g
+    return {"dtypes": list(dtypes), "batches": list(batches), "sizes": list(sizes),
+            "method": f"{warmup} warmup, {trials} trials x {repeat} calls, median, implementations alternating",
+            "reference_source": "reference VALIDATION.md:84-95 (A100 80GB PCIe) and benchmarks/matrix_exp.py",
+            "rows": rows}
 
 
 def main() -> int:
@@ -354,10 +493,13 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baselines")
+    ap.add_argument("--trials", type=int, default=5, help="the K timed steps are split into this many trials")
+    ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU leg (CPU baselines and parity)")
     ap.add_argument("--only", default=None, help="comma list of configs (c2,c3,c4,c5,c5f32,p8,c2s8)")
     ap.add_argument("--extras", action="store_true",
                     help="with --only: also run the reference table and the small-batch latency")
+    ap.add_argument("--sweep", action="store_true",
+                    help="reference table over B in {1,128,1024,65536} x {f32,f16,bf16} (the reference's sweep)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one device copy of exactly 64 MiB (profiler counter calibration)")
     args = ap.parse_args()
@@ -383,22 +525,32 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
     configs = (args.only or "c2,c3,c4,c5,c5f32,p8,c2s8").split(",")
-    results = {}
+    results, kept = {}, {}
     for name in configs:
         log(f"[bench] {name} ...")
-        results[name] = measure_config(name, torch, fh, args.steps, args.warmup, device)
+        results[name], k = measure_config(name, torch, fh, args.steps, args.warmup, args.trials, device,
+                                          keep=not args.skip_cpu and name != "c2s8")
+        if k:
+            kept[name] = k
         log(f"[bench] {name}: {json.dumps(results[name])}")
-        torch.cuda.empty_cache()
 
     head = results.get("c2")
+    cold = None
+    if head is not None:
+        log("[bench] cold c2 step ...")
+        cold = cold_step(torch, fh, args.steps, args.warmup, args.trials, device)
+        log(f"[bench] cold c2 step: {json.dumps(cold)}")
     table = latency = None
-    if args.only is None or args.extras:
+    if args.only is None or args.extras or args.sweep:
         # Not part of --only runs, so that a profile of one config holds only its own launches.
         log("[bench] reference table ...")
-        table = reference_table(torch, fh, device)
+        if args.sweep:
+            table = reference_table(torch, fh, device, batches=(1, 128, 1024, 65536), dtypes=("f32", "f16", "bf16"))
+        else:
+            table = reference_table(torch, fh, device)
         for row in table["rows"]:
-            log(f"[bench] reference table: n={row['n']:2} {row['mode']:16} {row['median_us']:9.1f} us "
-                f"(A100 {row['reference_a100_us']:8.1f} us, x{row['reference_time_over_ours']:.2f})")
+            log(f"[bench] reference table: n={row['n']:2} B={row['batch']:6} {row['dtype']:4} {row['mode']:16} "
+                f"{row['median_us']:9.1f} us (stock GPU {row['stock_gpu_us']:9.1f} us)")
         log("[bench] small-batch latency ...")
         latency = small_batch_latency(torch, fh, device)
         log(f"[bench] small-batch latency: {json.dumps(latency)}")
@@ -427,6 +579,8 @@ def main() -> int:
         b = 1 << 20
         bytes_bwd = b * 16 * 3 * 4
         achieved = head["bwd_kernel"]["achieved_gbs"]
+        line["trials"] = len(head["ms_step_trials"])
+        line["trials_ms"] = head["ms_step_trials"]
         line["roofline"] = {
             "bound": "hbm",
             "achieved": achieved,
@@ -437,13 +591,19 @@ def main() -> int:
             "traffic_source": "profiles/expm_p4_c2_hbm_traffic.md (FETCH_SIZE, WRITE_SIZE; copy-calibrated)",
             "kernel": "expm_p4_kernel<F32, Pair=true> (Frechet backward, P=4)",
             "algorithmic_bytes_per_launch": bytes_bwd,
-            "mean_launch_ms": head["ms_bwd_kernel"],
+            "median_launch_ms": head["ms_bwd_kernel"],
+            "launch_trials_ms": head["ms_bwd_trials"],
         }
         line["step_roofline_frac"] = head["roofline_frac_step"]
+        if cold is not None:
+            line["cold_step"] = cold
+            line["cold_over_warm"] = cold["ms_step"] / head["ms_step"]
     if not args.skip_cpu:
-        log("[bench] cpu baselines ...")
-        line["cpu_baseline"] = cpu_oracle_baseline(torch)
-        line["cpu_native_torch"] = cpu_native_torch(torch)
+        log("[bench] cpu leg ...")
+        leg = cpu_leg(torch, kept)
+        line["cpu_baseline"] = leg["cpu_baseline"]
+        line["cpu_oracle_port"] = leg["cpu_oracle_port"]
+        line["parity"] = leg["parity"]
     if latency is not None:
         line["small_batch_latency"] = latency
         line["reference_table"] = table

@@ -189,14 +189,14 @@ class _DualMatrixExp(torch.autograd.Function):
 
 
 def matrix_exp(input: torch.Tensor) -> torch.Tensor:
-    """Compute exp(input), accelerating ROCm [B, N, N] tensors with 2 <= N <= 32 on gfx950.
+    """exp(input) for batched square matrices; [B, N, N] (2 <= N <= 32) float32 / float16 /
+    bfloat16 tensors on a gfx950 device run the HIP kernels, anything else native PyTorch.
 
-    The HIP implementation accepts float32, float16, and bfloat16. Other
-    inputs use native PyTorch. An eligible input carrying a forward-mode
-    tangent gets its tangent from the Frechet kernel. Function transforms,
-    tensor subclasses and forward-mode inputs that are not eligible use native
-    operations; their GPU low-precision inputs are promoted to float32 for the
-    calculation and cast back on return.
+    Differentiable: the gradient is the structured Frechet derivative L(A^T, G) from the Frechet
+    kernel; a forward-mode tangent H on an eligible input is carried as L(A, H) from the same
+    kernel.  Inputs under functorch transforms, tensor subclasses, and dual inputs that are not
+    eligible take the native exponential; on the GPU their float16 / bfloat16 values are
+    evaluated in float32 and cast back.
     """
     # Check transforms before shape eligibility: vmap can hide batch dimensions.
     if isinstance(input, torch.Tensor) and (
@@ -225,11 +225,12 @@ class _MatrixExpMode(TorchFunctionMode):
 
 
 def use_backend() -> TorchFunctionMode:
-    """Route Python matrix-exp calls through flash-hypercons within a with block.
+    """Context manager: inside it, torch.linalg.matrix_exp, torch.matrix_exp and
+    Tensor.matrix_exp called from Python go through ``matrix_exp`` above.
 
-    Scopes nest and restore normal routing on exit, including exceptional exit.
-    Enter the scope around calls to compiled functions as well as eager calls.
-    Direct ATen/C++ calls are unaffected.
+    The mode is per thread and may be nested; leaving the block, normally or by an exception,
+    restores the previous routing.  Calls that Dynamo traces inside the block are captured as the
+    custom operator.  ATen or C++ callers of linalg_matrix_exp are not affected.
     """
     return _MatrixExpMode()
 

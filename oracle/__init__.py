@@ -22,6 +22,7 @@ from __future__ import annotations
 import ctypes
 import os
 import subprocess
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 import numpy as np
@@ -80,11 +81,29 @@ def _as_f32(a: np.ndarray) -> np.ndarray:
     return np.ascontiguousarray(a)
 
 
-def matrix_exp_f32(x: np.ndarray, g: np.ndarray | None = None):
+def default_threads() -> int:
+    """Host threads the checker may use: the process's CPU affinity, at most 16."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def _chunks(batch: int, threads: int):
+    threads = max(1, min(threads, batch // 4096 or 1))
+    step = -(-batch // threads)
+    return [(lo, min(batch, lo + step)) for lo in range(0, batch, step)]
+
+
+def matrix_exp_f32(x: np.ndarray, g: np.ndarray | None = None, threads: int = 1):
     """exp(x) (g None) or the U block of exp([[x, g], [0, x]]) for FP32 [B, n, n].
 
     Returns (FP32 result before output rounding, int32 s per matrix, FP64 norm).
-    s is -1 where the non-finite rule fired.
+    s is -1 where the non-finite rule fired.  ``threads`` > 1 splits the batch
+    into contiguous chunks run concurrently (the C code keeps no shared state
+    and ctypes releases the GIL); every matrix is computed independently, so
+    the result does not depend on the split.
     """
     x = _as_f32(x)
     if x.ndim != 3 or x.shape[-1] != x.shape[-2]:
@@ -97,17 +116,32 @@ def matrix_exp_f32(x: np.ndarray, g: np.ndarray | None = None):
     out = np.empty_like(x)
     s = np.empty(batch, np.int32)
     norm = np.empty(batch, np.float64)
-    if batch:
+
+    def run(lo_hi):
+        lo, hi = lo_hi
         rc = lib().fho_matrix_exp(
-            _ptr(x, ctypes.c_float), _ptr(g, ctypes.c_float), batch, n, _ptr(out, ctypes.c_float),
-            _ptr(s, ctypes.c_int32), _ptr(norm, ctypes.c_double),
+            _ptr(x[lo:hi], ctypes.c_float), None if g is None else _ptr(g[lo:hi], ctypes.c_float), hi - lo, n,
+            _ptr(out[lo:hi], ctypes.c_float), _ptr(s[lo:hi], ctypes.c_int32), _ptr(norm[lo:hi], ctypes.c_double),
         )
         if rc != 0:
             raise RuntimeError("fho_matrix_exp failed")
+
+    if batch:
+        _run_chunks(run, batch, threads)
     return out, s, norm
 
 
-def params_f32(x: np.ndarray, g: np.ndarray | None = None):
+def _run_chunks(run, batch: int, threads: int) -> None:
+    parts = _chunks(batch, threads)
+    if len(parts) == 1:
+        run(parts[0])
+        return
+    with ThreadPoolExecutor(max_workers=len(parts)) as pool:
+        for f in [pool.submit(run, p) for p in parts]:
+            f.result()
+
+
+def params_f32(x: np.ndarray, g: np.ndarray | None = None, threads: int = 1):
     """(s, FP64 norm) per matrix; the degree is always 18 for finite matrices."""
     x = _as_f32(x)
     batch, n = x.shape[0], x.shape[-1]
@@ -115,11 +149,16 @@ def params_f32(x: np.ndarray, g: np.ndarray | None = None):
         g = _as_f32(g)
     s = np.empty(batch, np.int32)
     norm = np.empty(batch, np.float64)
-    if batch:
-        rc = lib().fho_expm_params(_ptr(x, ctypes.c_float), _ptr(g, ctypes.c_float), batch, n,
-                                   _ptr(s, ctypes.c_int32), _ptr(norm, ctypes.c_double))
+
+    def run(lo_hi):
+        lo, hi = lo_hi
+        rc = lib().fho_expm_params(_ptr(x[lo:hi], ctypes.c_float), None if g is None else _ptr(g[lo:hi], ctypes.c_float),
+                                   hi - lo, n, _ptr(s[lo:hi], ctypes.c_int32), _ptr(norm[lo:hi], ctypes.c_double))
         if rc != 0:
             raise RuntimeError("fho_expm_params failed")
+
+    if batch:
+        _run_chunks(run, batch, threads)
     return s, norm
 
 
@@ -181,34 +220,32 @@ def round_to_dtype(out_f32: np.ndarray, dtype):
     raise TypeError(dtype)
 
 
-def torch_matrix_exp(x):
+def torch_matrix_exp(x, threads: int = 1):
     """Oracle forward on a torch tensor: (result in x.dtype on CPU, s int32 tensor)."""
     torch = _torch()
-    out, s, _ = matrix_exp_f32(tensor_to_f32(x))
+    out, s, _ = matrix_exp_f32(tensor_to_f32(x), threads=threads)
     return round_to_dtype(out, x.dtype), torch.from_numpy(s)
 
 
-def torch_frechet(x, g):
+def torch_frechet(x, g, threads: int = 1):
     """Oracle of the op ``_frechet(x, g)``: U block of exp([[x, g],[0, x]])."""
     torch = _torch()
-    out, s, _ = matrix_exp_f32(tensor_to_f32(x), tensor_to_f32(g))
+    out, s, _ = matrix_exp_f32(tensor_to_f32(x), tensor_to_f32(g), threads=threads)
     return round_to_dtype(out, x.dtype), torch.from_numpy(s)
 
 
-def torch_params(x, g=None):
+def torch_params(x, g=None, threads: int = 1):
     torch = _torch()
-    s, norm = params_f32(tensor_to_f32(x), None if g is None else tensor_to_f32(g))
+    s, norm = params_f32(tensor_to_f32(x), None if g is None else tensor_to_f32(g), threads=threads)
     return torch.from_numpy(s), torch.from_numpy(norm)
 
 
-def cpu_threads() -> int:
-    return 1  # the restatement is scalar C
 
 
 __all__ = [
     "THETA18", "DEGREE", "build", "matrix_exp_f32", "params_f32", "norm1", "squarings", "padded_size",
     "coefficients", "f32_to_bf16_bits", "tensor_to_f32", "round_to_dtype", "torch_matrix_exp",
-    "torch_frechet", "torch_params",
+    "torch_frechet", "torch_params", "default_threads",
 ]
 
 if os.environ.get("FHO_BUILD_ON_IMPORT"):

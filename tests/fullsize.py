@@ -1,0 +1,221 @@
+"""Full-size parity of one BASELINE workload: every matrix, both directions.
+
+Used by ``tests/test_full_parity.py`` (asserts) and by ``bench.py``'s CPU leg
+(reports the same counts in its JSON line).  For a workload (x, g) and the
+GPU's results of one forward + backward step it computes, over ALL matrices:
+
+* ``s`` of the kernels (``_expm_debug``) against the CPU restatement
+  (``oracle.params_f32``, threaded) -- forward on x, backward on (x^T, g);
+* bitwise mismatches of the results against the restatement's results
+  (``oracle.matrix_exp_f32``) -- zero is required where the kernel keeps the
+  reference's evaluation order (n <= 8), reported elsewhere;
+* the north-star tolerance against FP64 ``linalg_matrix_exp`` (evaluated on the
+  GPU in float64): per matrix, FP32 relative Frobenius error <= 1e-5 forward /
+  <= 1e-4 backward, FP16/BF16 every element within one output ulp of the
+  FP64 result (infinities matching).  Scaling and squaring at large s
+  amplifies FP32 rounding beyond this strict rule for the reference's own
+  arithmetic too, so the error is measured for the kernel AND for the
+  restatement on the same inputs: the number of matrices breaking the strict
+  rule, and per matrix the kernel's error over max(bound, the restatement's
+  error) -- the "excess over the reference".
+
+The oracle is test infrastructure; nothing here is part of the product path.
+"""
+
+from __future__ import annotations
+
+import torch
+
+import oracle
+from tests.reference import BWD_REL_FRO, FWD_REL_FRO, rel_frobenius, ulp
+
+AUTO = 0
+
+# Per-matrix sanity caps on the excess over the reference arithmetic (see direction_parity): far
+# above the scatter two FP32 summation orders show on the same matrix, far below any real mistake.
+EXCESS_LIMIT_F32 = 4.0  # ratio
+EXCESS_LIMIT_LOW = 2.0  # output ulps
+MEAN_ERROR_LIMIT = 1.05  # FP32 mean relative Frobenius error, kernel over restatement
+
+
+def fp64_reference(x, g=None, chunk: int = 1 << 16):
+    """FP64 exp(x) or L(x, g) = U block of exp([[x, g], [0, x]]), on x's device, in chunks."""
+    outs = []
+    n = x.shape[-1]
+    for lo in range(0, x.shape[0], chunk):
+        a = x[lo:lo + chunk].double()
+        if g is None:
+            outs.append(torch.linalg.matrix_exp(a))
+            continue
+        d = g[lo:lo + chunk].double()
+        block = torch.zeros(a.shape[0], 2 * n, 2 * n, dtype=torch.float64, device=a.device)
+        block[:, :n, :n] = a
+        block[:, n:, n:] = a
+        block[:, :n, n:] = d
+        outs.append(torch.linalg.matrix_exp(block)[:, :n, n:].contiguous())
+    return torch.cat(outs) if outs else torch.empty(0, n, n, dtype=torch.float64, device=x.device)
+
+
+# FP16/BF16 elements whose exact value lies within this relative distance of the dtype's overflow
+# threshold (max + half an ulp) may round to the largest finite value or to infinity: an FP32
+# evaluation error of a few hundred FP32 ulps decides which, for the reference's arithmetic too.
+OVERFLOW_BAND = 2.0**-10
+
+
+def error_ratio(actual, ref64, *, backward: bool, normwise: bool = False):
+    """Per-matrix error in units of the strict north-star bound (> 1: the matrix breaks it).
+
+    FP32: relative Frobenius error / (1e-5 forward, 1e-4 backward).  FP16/BF16: the largest
+    elementwise |actual - ref| / max(one ulp at max(|actual|, |ref|), one ulp of the matrix's
+    largest finite |ref|); elements at the overflow threshold (OVERFLOW_BAND) count as exact when
+    they hold the largest finite value or the infinity of the right sign.  Any other infinity
+    that the rounded reference does not have (or the reverse), or a NaN, makes the ratio
+    infinite.
+
+    ``normwise`` (FP16/BF16): each output is read as the interval of reals that round to it
+    (+inf: [threshold, inf)), its error is the distance from the exact value to that interval,
+    and the unit is one ulp at the matrix's largest |ref| over ALL entries, those beyond the
+    dtype's range included -- the scale at which an FP32 evaluation's error lives, for the
+    reference's arithmetic as well."""
+    ref64 = ref64.to(actual.device)
+    if actual.dtype == torch.float32:
+        return rel_frobenius(actual, ref64) / (BWD_REL_FRO if backward else FWD_REL_FRO)
+    finfo = torch.finfo(actual.dtype)
+    threshold = finfo.max + ulp(torch.tensor(finfo.max, dtype=torch.float64), actual.dtype).item() / 2
+    if normwise:
+        a = actual.double()
+        finite = a.isfinite()
+        half = torch.where(finite, ulp(a.abs(), actual.dtype) / 2, torch.zeros_like(a))
+        dist = torch.where(finite, ((a - ref64).abs() - half).clamp_min(0), torch.zeros_like(a))
+        dist = torch.where(a == float("inf"), (threshold - ref64).clamp_min(0), dist)
+        dist = torch.where(a == -float("inf"), (ref64 + threshold).clamp_min(0), dist)
+        dist = torch.where(a.isnan(), torch.full_like(a, float("inf")), dist)
+        unit = ulp(ref64.abs().flatten(-2).amax(-1), actual.dtype)
+        return dist.flatten(-2).amax(-1) / unit
+    at_edge = (ref64.abs() - threshold).abs() <= OVERFLOW_BAND * threshold
+    edge_ok = at_edge & ((actual.abs() == finfo.max) | actual.isinf()) & (actual.sign() == ref64.sign())
+    rounded = ref64.to(actual.dtype)
+    inf_ref = rounded.isinf()
+    bad_inf = ((actual.isinf() != inf_ref) | (inf_ref & (actual != rounded))) & ~edge_ok
+    broken = (bad_inf | actual.isnan()).flatten(-2).any(-1)
+    fin = ~inf_ref & ~actual.isinf()
+    act = torch.where(fin, actual.double(), torch.zeros_like(ref64))
+    fref = torch.where(fin, ref64, torch.zeros_like(ref64))
+    floor = ulp(torch.where(inf_ref, torch.zeros_like(ref64), ref64).abs().flatten(-2).amax(-1),
+                actual.dtype)[..., None, None]
+    tol = torch.maximum(ulp(torch.maximum(act.abs(), fref.abs()), actual.dtype), floor)
+    elem = torch.where(edge_ok, torch.zeros_like(ref64), (act - fref).abs() / tol)
+    ratio = elem.flatten(-2).amax(-1)
+    return torch.where(broken, torch.full_like(ratio, float("inf")), ratio)
+
+
+def strict_failures(actual, ref64, *, backward: bool):
+    """Per-matrix bool: the result breaks the strict north-star rule."""
+    return ~(error_ratio(actual, ref64, backward=backward) <= 1.0)
+
+
+def excess_over_reference(kernel_ratio, oracle_ratio, dtype):
+    """Per matrix, how much the kernel's error exceeds max(strict bound, the reference
+    arithmetic's own error on the same matrix).  FP32: the quotient of relative Frobenius errors
+    (<= 1: within the bound or no worse than the reference's evaluation).  FP16/BF16: the
+    difference of normwise ulp errors (error_ratio(normwise=True); <= 0: same), since one FP32
+    rounding difference can move an output by one ulp."""
+    floor = torch.clamp(oracle_ratio, min=1.0)
+    both_inf = kernel_ratio.isinf() & oracle_ratio.isinf()
+    if dtype == torch.float32:
+        return torch.where(both_inf, torch.ones_like(kernel_ratio), kernel_ratio / floor)
+    return torch.where(both_inf, torch.zeros_like(kernel_ratio), kernel_ratio - floor)
+
+
+def _bitwise_mismatches(actual, expected) -> int:
+    a = actual.cpu().double()
+    e = expected.double()
+    equal = (a == e) | (a.isnan() & e.isnan())
+    return int((~equal).flatten(-2).any(-1).sum())
+
+
+def _debug_launch(x, g):
+    import flash_hypercons  # noqa: F401  (registers the debug operators)
+
+    return torch.ops.flash_hypercons._expm_debug(x, g, AUTO)
+
+
+def direction_parity(x, g, out, *, threads: int | None = None, launch=None) -> dict:
+    """Parity of one direction over every matrix.  ``x`` is the operand the kernel saw
+    (forward: the input; backward: input^T), ``g`` the Frechet direction or None, ``out`` the
+    kernel's result on the GPU.  ``launch(x, g) -> (out, s)`` relaunches the kernels with the
+    per-matrix squaring counts (default: the ``_expm_debug`` operator)."""
+    threads = threads or oracle.default_threads()
+    backward = g is not None
+    dbg_out, s_kernel = (launch or _debug_launch)(x, g)
+    same_launch = bool(torch.equal(dbg_out, out))
+    xc = x.detach().cpu()
+    gc = None if g is None else g.detach().cpu()
+    ora_out, ora_s = (oracle.torch_matrix_exp(xc, threads=threads) if g is None
+                      else oracle.torch_frechet(xc, gc, threads=threads))
+    s_cpu = s_kernel.cpu().to(ora_s.dtype)
+    ref64 = fp64_reference(x, g)
+    finite = (ora_s >= 0).to(out.device)
+    ora_dev = ora_out.to(out.device)
+    k_ratio = error_ratio(out[finite], ref64[finite], backward=backward)
+    o_ratio = error_ratio(ora_dev[finite], ref64[finite], backward=backward)
+    if out.dtype == torch.float32:
+        excess = excess_over_reference(k_ratio, o_ratio, out.dtype)
+    else:
+        excess = excess_over_reference(error_ratio(out[finite], ref64[finite], backward=backward, normwise=True),
+                                       error_ratio(ora_dev[finite], ref64[finite], backward=backward,
+                                                   normwise=True), out.dtype)
+    worse = excess > (1.0 if out.dtype == torch.float32 else 0.0)
+    result = {
+        "matrices": int(x.shape[0]),
+        "s_mismatches": int((s_cpu != ora_s).sum()),
+        "s_max": int(ora_s.max()) if ora_s.numel() else 0,
+        "nonfinite_matrices": int((ora_s < 0).sum()),
+        "bitwise_mismatches_vs_oracle": _bitwise_mismatches(out, ora_out),
+        "strict_failures_kernel": int((~(k_ratio <= 1.0)).sum()),
+        "strict_failures_oracle": int((~(o_ratio <= 1.0)).sum()),
+        "matrices_worse_than_reference": int(worse.sum()),
+        "max_excess_over_reference": float(excess.max()) if excess.numel() else 0.0,
+        "excess_unit": "ratio" if out.dtype == torch.float32 else "output ulps",
+        "debug_launch_matches_op": same_launch,
+    }
+    if out.dtype == torch.float32:
+        err = rel_frobenius(out[finite], ref64[finite])
+        result["max_rel_frobenius"] = float(err.max()) if err.numel() else 0.0
+        result["mean_rel_frobenius"] = float(err.mean()) if err.numel() else 0.0
+        err_o = rel_frobenius(ora_dev[finite], ref64[finite])
+        result["oracle_mean_rel_frobenius"] = float(err_o.mean()) if err_o.numel() else 0.0
+    return result
+
+
+def check(report: dict, n: int) -> list[str]:
+    """The gate applied to one direction's report; returns the reasons it fails (empty: pass).
+
+    * s bit-identical to the restatement for every matrix;
+    * n <= 8: every result bit-identical to the restatement;
+    * no more matrices outside the strict north-star rule than the restatement has;
+    * FP32: mean relative Frobenius error at most 1.05x the restatement's;
+    * per matrix, the error above max(strict bound, restatement's error) stays under the sanity
+      cap (4x in FP32, 2 output ulps in FP16/BF16)."""
+    why = []
+    if report["s_mismatches"]:
+        why.append(f"{report['s_mismatches']} squaring counts differ")
+    if n <= 8 and report["bitwise_mismatches_vs_oracle"]:
+        why.append(f"{report['bitwise_mismatches_vs_oracle']} results differ in bits")
+    if report["strict_failures_kernel"] > report["strict_failures_oracle"]:
+        why.append(f"{report['strict_failures_kernel']} strict failures vs {report['strict_failures_oracle']}")
+    if "mean_rel_frobenius" in report and report["mean_rel_frobenius"] > MEAN_ERROR_LIMIT * report[
+            "oracle_mean_rel_frobenius"] + 1e-12:
+        why.append("mean error above the restatement's")
+    limit = EXCESS_LIMIT_F32 if report["excess_unit"] == "ratio" else EXCESS_LIMIT_LOW
+    if not report["max_excess_over_reference"] <= limit:
+        why.append(f"excess over the restatement {report['max_excess_over_reference']} > {limit}")
+    if not report["debug_launch_matches_op"]:
+        why.append("the debug launch differs from the operator's result")
+    return why
+
+
+def workload_parity(x, g, y, grad, *, threads: int | None = None, launch=None) -> dict:
+    """Both directions of one step: forward exp(x) = y; backward L(x^T, g) = grad."""
+    return {"forward": direction_parity(x, None, y, threads=threads, launch=launch),
+            "backward": direction_parity(x.mT, g, grad, threads=threads, launch=launch)}

@@ -37,6 +37,7 @@ KERNEL_SOURCES = [
     "expm_oct.hip",
     "expm_tile.hip",
     "expm_params.hip",
+    "hc_mix.hip",
     "fh_capi.cpp",
 ]
 

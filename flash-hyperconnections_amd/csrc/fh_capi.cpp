@@ -115,9 +115,40 @@ int launch(const void* input, const int64_t input_strides[3], int input_neg, con
   return FH_OK;
 }
 
+// Operands of the fused stream mixing: H any strides; X (and dY) [B, n, C]
+// with contiguous, 16-byte aligned rows of a whole number of 16-byte vectors,
+// each token's rows spanning less than 2 GiB.
+int validate_hc(const void* h, const int64_t* hs, const void* x, const int64_t* xs, const void* g, const int64_t* gs,
+                const void* out, int dtype, int64_t batch, int n, int64_t cols) {
+  if (n < 2 || n > 4 || (dtype != FH_DTYPE_F32 && dtype != FH_DTYPE_BF16 && dtype != FH_DTYPE_F16) || batch < 0 ||
+      cols < 1)
+    return fail(FH_ERR_INVALID_ARGUMENT,
+                "hc_mix: expected H [B, n, n] and X [B, n, C] with 2 <= n <= 4, C >= 1, in float32, float16, or "
+                "bfloat16");
+  if (batch == 0) return FH_OK;
+  if (h == nullptr || hs == nullptr || x == nullptr || xs == nullptr || out == nullptr)
+    return fail(FH_ERR_INVALID_ARGUMENT, "hc_mix: null pointer");
+  const int64_t es = element_size(dtype);
+  const int64_t v = 16 / es;
+  auto rows_ok = [&](const void* p, const int64_t* st) {
+    constexpr int64_t kSpan = int64_t{1} << 31;  // bytes one token's rows may span (32-bit buffer offsets)
+    return aligned(p, 16) && st[2] == 1 && st[0] >= 0 && st[1] >= 0 && st[0] % v == 0 && st[1] % v == 0 &&
+           cols % v == 0 && st[1] < kSpan && cols < kSpan && ((n - 1) * st[1] + cols) * es < kSpan;
+  };
+  if (!rows_ok(x, xs) || (g != nullptr && (gs == nullptr || !rows_ok(g, gs))) || !aligned(out, 16))
+    return fail(FH_ERR_INVALID_ARGUMENT,
+                "hc_mix: X and dY need contiguous, 16-byte aligned rows whose length C and strides are multiples of " +
+                    std::to_string(v) + " elements");
+  return FH_OK;
+}
+
 }  // namespace
 
 namespace fh {
+
+Operand hc_operand(const void* h, const int64_t strides[3], int neg, int dtype) {
+  return make_operand(h, strides, neg, dtype, 0);
+}
 
 int64_t resident_blocks(const void* kernel, int block) {
   int device = 0;
@@ -171,6 +202,32 @@ int fh_expm_params(const void* input, const int64_t input_strides[3], int input_
   args.batch = batch;
   args.n = n;
   const hipError_t err = fh::launch_params(args, dtype, pair, params, norms, stream);
+  if (err != hipSuccess) return fail(FH_ERR_LAUNCH, std::string("kernel launch failed: ") + hipGetErrorString(err));
+  g_error.clear();
+  return FH_OK;
+}
+
+int fh_hc_mix(const void* h, const int64_t h_strides[3], int h_neg, const void* x, const int64_t x_strides[3],
+              void* y, float* e_out, int dtype, int64_t batch, int n, int64_t cols, hipStream_t stream) {
+  int rc = validate_hc(h, h_strides, x, x_strides, nullptr, nullptr, y, dtype, batch, n, cols);
+  if (rc != FH_OK || batch == 0) return rc;
+  const hipError_t err = fh::launch_hc_mix(fh::hc_operand(h, h_strides, h_neg, dtype), x, x_strides, nullptr,
+                                           nullptr, y, nullptr, e_out, dtype, batch, n, cols, stream);
+  if (err != hipSuccess) return fail(FH_ERR_LAUNCH, std::string("kernel launch failed: ") + hipGetErrorString(err));
+  g_error.clear();
+  return FH_OK;
+}
+
+int fh_hc_mix_backward(const void* h, const int64_t h_strides[3], int h_neg, const void* x,
+                       const int64_t x_strides[3], const void* grad, const int64_t grad_strides[3], void* dh,
+                       void* dx, float* de_out, int dtype, int64_t batch, int n, int64_t cols, hipStream_t stream) {
+  int rc = validate_hc(h, h_strides, x, x_strides, grad, grad_strides, dx, dtype, batch, n, cols);
+  if (rc != FH_OK) return rc;
+  if (batch > 0 && (grad == nullptr || dh == nullptr))
+    return fail(FH_ERR_INVALID_ARGUMENT, "hc_mix: null grad or dh pointer");
+  if (batch == 0) return FH_OK;
+  const hipError_t err = fh::launch_hc_mix(fh::hc_operand(h, h_strides, h_neg, dtype), x, x_strides, grad,
+                                           grad_strides, dx, dh, de_out, dtype, batch, n, cols, stream);
   if (err != hipSuccess) return fail(FH_ERR_LAUNCH, std::string("kernel launch failed: ") + hipGetErrorString(err));
   g_error.clear();
   return FH_OK;

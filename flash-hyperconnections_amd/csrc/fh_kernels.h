@@ -17,6 +17,16 @@ hipError_t launch_p4(const ExpmArgs& args, int dtype, bool pair, hipStream_t str
 hipError_t launch_oct(const ExpmArgs& args, int dtype, bool pair, hipStream_t stream);
 // P in {16, 32}: one wavefront per matrix on 16x16x4 / 32x32x2 MFMA.
 hipError_t launch_tile(const ExpmArgs& args, int dtype, int P, bool pair, hipStream_t stream);
+// Fused hyper-connection stream mixing (n = 2..4): gy == nullptr selects the
+// forward Y = exp(H) X into `out`; otherwise the backward dX = exp(H)^T dY into
+// `out` and dH = L(H^T, dY X^T) into `dh`.  `xs` / `gs`: element strides
+// (token, row) of X / dY, whose columns are contiguous.  `aux` (may be null):
+// FP32 [B, n, n] copy of exp(H) (forward) or dY X^T (backward).
+// H of the stream mixing as an element-class operand.
+Operand hc_operand(const void* h, const int64_t strides[3], int neg, int dtype);
+hipError_t launch_hc_mix(const Operand& h, const void* x, const int64_t* xs, const void* gy, const int64_t* gs,
+                         void* out, void* dh, float* aux, int dtype, int64_t batch, int n, int64_t cols,
+                         hipStream_t stream);
 // (degree, s) and FP64 norm per matrix.
 hipError_t launch_params(const ExpmArgs& args, int dtype, bool pair, int32_t* params, double* norms,
                          hipStream_t stream);

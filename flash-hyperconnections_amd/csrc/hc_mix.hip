@@ -1,0 +1,409 @@
+// Hyper-connection stream mixing with the exponential fused in:
+//   forward   Y_b = exp(H_b) X_b                         H [B, n, n], X [B, n, C]
+//   backward  dX_b = exp(H_b)^T dY_b,
+//             dE_b = dY_b X_b^T,  dH_b = L(H_b^T, dE_b)   (the gradient of exp)
+// for n = 2..4 residual streams and any width C.  Nothing of the reference
+// fuses this; its matrix_exp (ops/matrix_exp/__init__.py:80-97) returns
+// exp(H) to the caller, who multiplies.  Here exp(H_b) never leaves the chip:
+//
+// * A wavefront takes kTokens consecutive tokens.  Lane l computes exp(H) of
+//   token l % kTokens with the per-lane P == 4 code (p4_lane.h, the same
+//   arithmetic as the matrix-exponential kernel, so E is bit-identical to it)
+//   and parks it in the wavefront's LDS.
+// * The wavefront then streams each token's rows: every lane loads 16 bytes
+//   of each of the n rows per chunk (the whole wavefront covers 1 KB of each
+//   row per chunk, coalesced), multiplies by E read back from LDS (one
+//   broadcast read per token) and stores 16 bytes of each output row.  Rows
+//   are addressed through a buffer resource rebased per token in SGPRs, so no
+//   VALU address arithmetic is needed and offsets never exceed one token.
+// * The backward accumulates dE_b = dY_b X_b^T per lane over its columns (in
+//   column order), reduces the 16 partial sums across the wavefront with a
+//   fixed exchange tree (the result does not depend on anything but the
+//   data), parks dE_b in LDS, and after its tokens each lane runs the P == 4
+//   Frechet polynomial on (H^T, dE) of one token -- the same arithmetic as the
+//   Frechet kernel.
+//
+// Both directions are bound by HBM traffic (16 FMAs per 2n elements moved
+// forward, 32 per 3n backward); the exponential and Frechet work per token is
+// small beside C >= a few hundred columns.
+#include "p4_lane.h"
+
+namespace fh {
+namespace {
+
+using namespace p4;
+
+constexpr int kWaves = 4;   // wavefronts per workgroup
+constexpr int kTokens = 8;  // tokens per wavefront
+
+struct HcArgs {
+  Operand h;        // [B, n, n]
+  const void* x;    // [B, n, C], unit column stride
+  int64_t xb, xr;   // element strides of X (token, row)
+  const void* gy;   // backward: dY [B, n, C], unit column stride
+  int64_t gb, gr;
+  void* out;        // forward: Y, backward: dX; contiguous [B, n, C]
+  void* dh;         // backward: dH, contiguous [B, n, n]
+  float* aux;       // optional FP32 [B, n, n]: exp(H) (forward) or dE (backward)
+  int64_t batch;
+  int64_t cols;
+  int n;
+};
+
+// Buffer resource over `bytes` bytes at `base` + `offset_elems` elements (uniform).
+template <typename T>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rebased(const void* base, int64_t offset_elems, int64_t bytes) {
+  const char* p = static_cast<const char*>(base) + offset_elems * static_cast<int64_t>(sizeof(typename T::storage));
+  return make_rsrc(p, static_cast<uint32_t>(bytes));
+}
+
+// 16 bytes of storage as FP32 values (4 for FP32, 8 for FP16/BF16).
+template <typename T>
+struct Vec {
+  static constexpr int V = 16 / static_cast<int>(sizeof(typename T::storage));
+  float f[V];
+};
+
+template <typename T>
+__device__ __forceinline__ Vec<T> unpack(U32x4 w) {
+  using S = typename T::storage;
+  Vec<T> r;
+#pragma unroll
+  for (int i = 0; i < Vec<T>::V; ++i) {
+    if constexpr (sizeof(S) == 4) {
+      r.f[i] = __uint_as_float(w[i]);
+    } else {
+      const uint16_t h = static_cast<uint16_t>(w[i >> 1] >> (16 * (i & 1)));
+      r.f[i] = to_f32<T>(__builtin_bit_cast(S, h));
+    }
+  }
+  return r;
+}
+
+template <typename T>
+__device__ __forceinline__ U32x4 pack(const Vec<T>& v) {
+  using S = typename T::storage;
+  U32x4 w;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (sizeof(S) == 4) {
+      w[i] = __float_as_uint(v.f[i]);
+    } else {
+      w[i] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(v.f[2 * i]))) |
+             (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(v.f[2 * i + 1]))) << 16);
+    }
+  }
+  return w;
+}
+
+__device__ __forceinline__ U32x4 load16(__amdgpu_buffer_rsrc_t rs, int32_t voff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 0, 0);
+}
+
+__device__ __forceinline__ void store16(U32x4 w, __amdgpu_buffer_rsrc_t rs, int32_t voff) {
+  __builtin_amdgcn_raw_buffer_store_b128(w, rs, voff, 0, 0);
+}
+
+// exp(H) of token `b` for this lane (valid lanes), NaN for a non-finite H
+// (csrc/MatrixExpSmall.cuh:126-140).
+template <typename T, int N>
+__device__ __forceinline__ M4 exp_of_token(const Operand& h, int64_t b, bool valid) {
+  PM<false> cur;
+  if (valid) {
+    cur.d = load_elements<T>(h, b, N);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) cur.d.v[e] = 0.f;
+  }
+  M4 e;
+  const int s = expm_lane<false>(cur, h.sign, 1.f, [&](const M4& out) { e = out; });
+  if (s < 0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) e.v[i] = __builtin_nanf("");
+  }
+  return e;
+}
+
+// The wavefront's tokens [t0, t0 + kTokens): lane l holds exp(H) of token
+// t0 + l % kTokens and lanes below kTokens park it in `etile` (16 floats per
+// token); `aux` (optional) receives it in FP32.
+template <typename T, int N>
+__device__ __forceinline__ void exp_tokens(const HcArgs& a, int64_t t0, int lane, float* etile) {
+  const int64_t b = t0 + (lane & (kTokens - 1));
+  const bool valid = b < a.batch;
+  const M4 e = exp_of_token<T, N>(a.h, b, valid);
+  if (lane < kTokens) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<float4*>(etile + 16 * lane + 4 * q) =
+          make_float4(e.v[4 * q], e.v[4 * q + 1], e.v[4 * q + 2], e.v[4 * q + 3]);
+    if (a.aux && valid) {
+#pragma unroll
+      for (int i = 0; i < N; ++i)
+#pragma unroll
+        for (int j = 0; j < N; ++j) a.aux[b * N * N + i * N + j] = e.v[4 * i + j];
+    }
+  }
+  lds_order();
+}
+
+__device__ __forceinline__ M4 read_token(const float* tile, int i) {
+  M4 m;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float4 v = *reinterpret_cast<const float4*>(tile + 16 * i + 4 * q);
+    m.v[4 * q] = v.x;
+    m.v[4 * q + 1] = v.y;
+    m.v[4 * q + 2] = v.z;
+    m.v[4 * q + 3] = v.w;
+  }
+  return m;
+}
+
+// 16-byte column chunks per lane in flight per token: the forward keeps four
+// (n loads each); the backward, which loads X and dY, two -- so that it fits
+// two wavefronts per SIMD beside the Frechet polynomial's registers.
+constexpr int kChunks = 4;
+constexpr int kChunksBwd = 2;
+
+// Forward: Y_b = E_b X_b, row i of Y = sum_k E[i][k] X[k] (fmaf chain k = 0..n-1 from +0).
+template <typename T, int N>
+__global__ __launch_bounds__(64 * kWaves) void hc_mix_fwd_kernel(HcArgs a) {
+  __shared__ __attribute__((aligned(16))) float etile_mem[kWaves][kTokens * 16];
+  constexpr int es = static_cast<int>(sizeof(typename T::storage));
+  constexpr int V = Vec<T>::V;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  float* etile = etile_mem[wave];
+  const int64_t blocks = (a.batch + kTokens - 1) / kTokens;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kWaves;
+  const int64_t span = static_cast<int64_t>(64) * V * kChunks;  // columns per pass
+  for (int64_t blk = static_cast<int64_t>(blockIdx.x) * kWaves + wave; blk < blocks; blk += stride) {
+    const int64_t t0 = blk * kTokens;
+    exp_tokens<T, N>(a, t0, lane, etile);
+    const int ntok = static_cast<int>(a.batch - t0 < kTokens ? a.batch - t0 : kTokens);
+    for (int i = 0; i < ntok; ++i) {
+      const int64_t b = t0 + i;
+      const M4 e = read_token(etile, i);
+      const __amdgpu_buffer_rsrc_t xs = rebased<T>(a.x, b * a.xb, ((N - 1) * a.xr + a.cols) * es);
+      const __amdgpu_buffer_rsrc_t ys = rebased<T>(a.out, b * N * a.cols, N * a.cols * es);
+      for (int64_t c0 = 0; c0 < a.cols; c0 += span) {
+        U32x4 raw[kChunks][N];
+#pragma unroll
+        for (int u = 0; u < kChunks; ++u) {
+          const int64_t c = c0 + (u * 64 + lane) * V;
+#pragma unroll
+          for (int k = 0; k < N; ++k)
+            raw[u][k] = c < a.cols ? load16(xs, static_cast<int32_t>((k * a.xr + c) * es)) : U32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < kChunks; ++u) {
+          const int64_t c = c0 + (u * 64 + lane) * V;
+          Vec<T> xv[N];
+#pragma unroll
+          for (int k = 0; k < N; ++k) xv[k] = unpack<T>(raw[u][k]);
+#pragma unroll
+          for (int i2 = 0; i2 < N; ++i2) {
+            Vec<T> y;
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+              float acc = __builtin_fmaf(e.v[4 * i2], xv[0].f[v], 0.f);
+#pragma unroll
+              for (int k = 1; k < N; ++k) acc = __builtin_fmaf(e.v[4 * i2 + k], xv[k].f[v], acc);
+              y.f[v] = acc;
+            }
+            if (c < a.cols) store16(pack<T>(y), ys, static_cast<int32_t>((i2 * a.cols + c) * es));
+          }
+        }
+      }
+    }
+    lds_order();
+  }
+}
+
+// Sum of 16 per-lane values over the wavefront, reduce-scatter style: after
+// exchanging halves with the lane 1, 2, 4, 8 apart (keeping the half this
+// lane's bit selects) every lane of a 16-lane row holds the row's sum of one
+// entry, entry = bit-reverse(lane & 15); two more exchanges (16, 32 apart) add
+// the rows.  Fixed order: every entry's sum is ((r0 + r1) + (r2 + r3)) of
+// fixed per-row trees.  Returns the total of entry bitrev4(lane & 15).
+__device__ __forceinline__ float wave_sum16(const float (&v)[16], int lane) {
+  float a[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) a[e] = v[e];
+#pragma unroll
+  for (int step = 0; step < 4; ++step) {
+    const int half = 8 >> step;
+    const bool upper = (lane >> step) & 1;
+#pragma unroll
+    for (int j = 0; j < half; ++j) {
+      const float keep = upper ? a[j + half] : a[j];
+      const float send = upper ? a[j] : a[j + half];
+      a[j] = keep + __shfl_xor(send, 1 << step);
+    }
+  }
+  float t = a[0] + __shfl_xor(a[0], 16);
+  return t + __shfl_xor(t, 32);
+}
+
+__device__ __forceinline__ int bitrev4(int x) { return ((x & 1) << 3) | ((x & 2) << 1) | ((x & 4) >> 1) | ((x & 8) >> 3); }
+
+// Backward: dX row k = sum_r E[r][k] dY[r] (fmaf chain r = 0..n-1 from +0);
+// dE[r][k] = sum_c dY[r][c] X[k][c] (per lane in column order, then
+// wave_sum16); dH = L(H^T, dE).
+template <typename T, int N>
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 8))) void hc_mix_bwd_kernel(HcArgs a) {
+  __shared__ __attribute__((aligned(16))) float etile_mem[kWaves][kTokens * 16];
+  __shared__ __attribute__((aligned(16))) float gtile_mem[kWaves][kTokens * 16];
+  constexpr int es = static_cast<int>(sizeof(typename T::storage));
+  constexpr int V = Vec<T>::V;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  float* etile = etile_mem[wave];
+  float* gtile = gtile_mem[wave];
+  const int64_t blocks = (a.batch + kTokens - 1) / kTokens;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kWaves;
+  const int64_t span = static_cast<int64_t>(64) * V * kChunksBwd;
+  for (int64_t blk = static_cast<int64_t>(blockIdx.x) * kWaves + wave; blk < blocks; blk += stride) {
+    const int64_t t0 = blk * kTokens;
+    exp_tokens<T, N>(a, t0, lane, etile);
+    const int ntok = static_cast<int>(a.batch - t0 < kTokens ? a.batch - t0 : kTokens);
+    for (int i = 0; i < ntok; ++i) {
+      const int64_t b = t0 + i;
+      const M4 e = read_token(etile, i);
+      const __amdgpu_buffer_rsrc_t xs = rebased<T>(a.x, b * a.xb, ((N - 1) * a.xr + a.cols) * es);
+      const __amdgpu_buffer_rsrc_t gs = rebased<T>(a.gy, b * a.gb, ((N - 1) * a.gr + a.cols) * es);
+      const __amdgpu_buffer_rsrc_t ds = rebased<T>(a.out, b * N * a.cols, N * a.cols * es);
+      float acc[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) acc[q] = 0.f;
+      for (int64_t c0 = 0; c0 < a.cols; c0 += span) {
+        U32x4 xr[kChunksBwd][N], gr[kChunksBwd][N];
+#pragma unroll
+        for (int u = 0; u < kChunksBwd; ++u) {
+          const int64_t c = c0 + (u * 64 + lane) * V;
+#pragma unroll
+          for (int k = 0; k < N; ++k) {
+            xr[u][k] = c < a.cols ? load16(xs, static_cast<int32_t>((k * a.xr + c) * es)) : U32x4{0, 0, 0, 0};
+            gr[u][k] = c < a.cols ? load16(gs, static_cast<int32_t>((k * a.gr + c) * es)) : U32x4{0, 0, 0, 0};
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kChunksBwd; ++u) {
+          const int64_t c = c0 + (u * 64 + lane) * V;
+          Vec<T> xv[N], gv[N];
+#pragma unroll
+          for (int k = 0; k < N; ++k) {
+            xv[k] = unpack<T>(xr[u][k]);
+            gv[k] = unpack<T>(gr[u][k]);
+          }
+#pragma unroll
+          for (int k = 0; k < N; ++k) {
+            Vec<T> dx;
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+              float d = __builtin_fmaf(e.v[k], gv[0].f[v], 0.f);
+#pragma unroll
+              for (int r = 1; r < N; ++r) d = __builtin_fmaf(e.v[4 * r + k], gv[r].f[v], d);
+              dx.f[v] = d;
+            }
+            if (c < a.cols) store16(pack<T>(dx), ds, static_cast<int32_t>((k * a.cols + c) * es));
+          }
+#pragma unroll
+          for (int r = 0; r < N; ++r)
+#pragma unroll
+            for (int k = 0; k < N; ++k)
+#pragma unroll
+              for (int v = 0; v < V; ++v) acc[4 * r + k] = __builtin_fmaf(gv[r].f[v], xv[k].f[v], acc[4 * r + k]);
+        }
+      }
+      const float total = wave_sum16(acc, lane);
+      if (lane < 16) gtile[16 * i + bitrev4(lane)] = total;
+    }
+    lds_order();
+    // L(H^T, dE) of token t0 + lane % kTokens.
+    const int64_t b = t0 + (lane & (kTokens - 1));
+    const bool valid = b < a.batch;
+    PM<true> cur;
+    if (valid) {
+      const M4 h = load_elements<T>(a.h, b, N);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) cur.d.v[4 * r + c] = h.v[4 * c + r];
+      cur.u = read_token(gtile, lane & (kTokens - 1));
+    } else {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        cur.d.v[q] = 0.f;
+        cur.u.v[q] = 0.f;
+      }
+    }
+    M4 dh;
+    const int s = expm_lane<true>(cur, a.h.sign, 1.f, [&](const M4& out) { dh = out; });
+    if (s < 0) {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) dh.v[q] = __builtin_nanf("");
+    }
+    if (lane < kTokens && valid) {
+      store_elements<T>(a.dh, b, N, dh);
+      if (a.aux) {
+#pragma unroll
+        for (int r = 0; r < N; ++r)
+#pragma unroll
+          for (int k = 0; k < N; ++k) a.aux[b * N * N + r * N + k] = cur.u.v[4 * r + k];
+      }
+    }
+    lds_order();
+  }
+}
+
+template <typename K>
+hipError_t launch_waves(K kernel, const HcArgs& a, hipStream_t stream) {
+  const int64_t blocks = (a.batch + kTokens - 1) / kTokens;
+  const int64_t resident = resident_blocks(reinterpret_cast<const void*>(kernel), 64 * kWaves);
+  int64_t grid = (blocks + kWaves - 1) / kWaves;
+  if (grid > resident) grid = resident;
+  if (grid < 1) grid = 1;
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(64 * kWaves), 0, stream, a);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_t(const HcArgs& a, bool backward, hipStream_t stream) {
+  switch (a.n) {
+    case 2:
+      return backward ? launch_waves(hc_mix_bwd_kernel<T, 2>, a, stream) : launch_waves(hc_mix_fwd_kernel<T, 2>, a, stream);
+    case 3:
+      return backward ? launch_waves(hc_mix_bwd_kernel<T, 3>, a, stream) : launch_waves(hc_mix_fwd_kernel<T, 3>, a, stream);
+    default:
+      return backward ? launch_waves(hc_mix_bwd_kernel<T, 4>, a, stream) : launch_waves(hc_mix_fwd_kernel<T, 4>, a, stream);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_hc_mix(const Operand& h, const void* x, const int64_t* xs, const void* gy, const int64_t* gs,
+                         void* out, void* dh, float* aux, int dtype, int64_t batch, int n, int64_t cols,
+                         hipStream_t stream) {
+  HcArgs a;
+  a.h = h;
+  a.x = x;
+  a.xb = xs[0];
+  a.xr = xs[1];
+  a.gy = gy;
+  a.gb = gs ? gs[0] : 0;
+  a.gr = gs ? gs[1] : 0;
+  a.out = out;
+  a.dh = dh;
+  a.aux = aux;
+  a.batch = batch;
+  a.cols = cols;
+  a.n = n;
+  const bool backward = gy != nullptr;
+  if (dtype == F32::code) return launch_t<F32>(a, backward, stream);
+  if (dtype == BF16::code) return launch_t<BF16>(a, backward, stream);
+  return launch_t<F16>(a, backward, stream);
+}
+
+}  // namespace fh

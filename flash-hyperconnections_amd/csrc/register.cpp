@@ -1,7 +1,9 @@
 // PyTorch-ROCm operator registration for flash_hypercons (the counterpart of
 // the reference's csrc/register.cpp and the ATen half of csrc/matrix_exp.cu).
 //
-// Schemas are the reference's (csrc/register.cpp:10-13) plus two debug ops.
+// Schemas are the reference's (csrc/register.cpp:10-13) plus two debug ops and
+// the fused hyper-connection stream mixing (_hc_mix, its backward and a debug
+// variant), which has no counterpart in the reference.
 // The implementations sit on the CUDA dispatch key, which ROCm tensors use.
 // Each one checks its inputs with the reference's messages
 // (csrc/matrix_exp.cu:52-59), allocates the contiguous output in the input
@@ -121,6 +123,94 @@ std::tuple<at::Tensor, at::Tensor> expm_params_hip(const at::Tensor& a, const st
   return {params, norms};
 }
 
+// ---- fused hyper-connection stream mixing ---------------------------------
+
+void check_mix(const at::Tensor& h, const at::Tensor& x) {
+  TORCH_CHECK(h.is_cuda() && h.layout() == at::kStrided && h.dim() == 3 && h.size(-1) == h.size(-2) &&
+                  h.size(-1) >= 2 && h.size(-1) <= 4 &&
+                  (h.scalar_type() == at::kFloat || h.scalar_type() == at::kHalf ||
+                   h.scalar_type() == at::kBFloat16),
+              "mix_streams: expected a strided CUDA [B, n, n] tensor h, 2 <= n <= 4, in float32, float16, or "
+              "bfloat16");
+  TORCH_CHECK(x.device() == h.device() && x.scalar_type() == h.scalar_type() && x.layout() == at::kStrided &&
+                  x.dim() == 3 && x.size(0) == h.size(0) && x.size(1) == h.size(1) && x.size(2) >= 1,
+              "mix_streams: expected x [B, n, C] of h's dtype and device, C >= 1");
+}
+
+// Rows contiguous, 16-byte aligned, strides and C in whole 16-byte vectors:
+// what the kernel reads in place; anything else is copied once.
+at::Tensor streamable(const at::Tensor& x) {
+  const int64_t v = 16 / static_cast<int64_t>(x.element_size());
+  const bool ok = !x.is_neg() && x.stride(2) == 1 && x.stride(1) % v == 0 && x.stride(0) % v == 0 &&
+                  x.stride(0) >= 0 && x.stride(1) >= 0 && x.size(2) % v == 0 &&
+                  reinterpret_cast<uintptr_t>(x.const_data_ptr()) % 16 == 0;
+  if (ok) return x;
+  at::Tensor c = x.resolve_neg().contiguous();
+  if (x.size(2) % v == 0 && reinterpret_cast<uintptr_t>(c.const_data_ptr()) % 16 == 0) return c;
+  // C not a whole number of vectors: pad the rows (the padding is never read back).
+  const int64_t padded = (x.size(2) + v - 1) / v * v;
+  at::Tensor p = at::zeros({x.size(0), x.size(1), padded}, x.options());
+  p.narrow(2, 0, x.size(2)).copy_(c);
+  return p;
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor> mix_run(const at::Tensor& h, const at::Tensor& x,
+                                                       const std::optional<at::Tensor>& grad, bool want_aux) {
+  check_mix(h, x);
+  if (grad) TORCH_CHECK(grad->sizes() == x.sizes() && grad->device() == x.device() &&
+                            grad->scalar_type() == x.scalar_type(),
+                        "mix_streams: grad must match x");
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(h.device());
+  const int64_t B = h.size(0), n = h.size(1), C = x.size(2);
+  const at::Tensor xs = streamable(x);
+  const int64_t Cp = xs.size(2);
+  at::Tensor out = at::empty({B, n, Cp}, x.options());
+  at::Tensor dh = grad ? at::empty({B, n, n}, h.options()) : at::Tensor();
+  at::Tensor aux = want_aux ? at::empty({B, n, n}, h.options().dtype(at::kFloat)) : at::Tensor();
+  if (B > 0) {
+    const View hv = view_of(h);
+    const int64_t x_strides[3] = {xs.stride(0), xs.stride(1), xs.stride(2)};
+    float* aux_ptr = want_aux ? aux.mutable_data_ptr<float>() : nullptr;
+    if (grad) {
+      at::Tensor gs = streamable(*grad);
+      if (gs.size(2) != Cp) {  // x needed padding that grad did not: pad grad alike
+        at::Tensor p = at::zeros({B, n, Cp}, gs.options());
+        p.narrow(2, 0, C).copy_(gs.narrow(2, 0, C));
+        gs = p;
+      }
+      const int64_t g_strides[3] = {gs.stride(0), gs.stride(1), gs.stride(2)};
+      check_status(fh_hc_mix_backward(hv.data, hv.strides, hv.neg, xs.const_data_ptr(), x_strides,
+                                      gs.const_data_ptr(), g_strides, dh.mutable_data_ptr(), out.mutable_data_ptr(),
+                                      aux_ptr, dtype_code(h.scalar_type()), B, static_cast<int>(n), Cp,
+                                      current_stream()));
+    } else {
+      check_status(fh_hc_mix(hv.data, hv.strides, hv.neg, xs.const_data_ptr(), x_strides, out.mutable_data_ptr(),
+                             aux_ptr, dtype_code(h.scalar_type()), B, static_cast<int>(n), Cp, current_stream()));
+    }
+  }
+  if (Cp != C) out = out.narrow(2, 0, C).contiguous();
+  return {out, dh, aux};
+}
+
+at::Tensor hc_mix_hip(const at::Tensor& h, const at::Tensor& x) {
+  return std::get<0>(mix_run(h, x, std::nullopt, false));
+}
+
+std::tuple<at::Tensor, at::Tensor> hc_mix_backward_hip(const at::Tensor& h, const at::Tensor& x,
+                                                       const at::Tensor& grad) {
+  auto r = mix_run(h, x, grad, false);
+  return {std::get<1>(r), std::get<0>(r)};
+}
+
+// Debug: (y or dx, dh or empty, FP32 exp(h) or dE) -- the values the fused
+// kernels keep on chip, for checking against the restatement.
+std::tuple<at::Tensor, at::Tensor, at::Tensor> hc_mix_aux_hip(const at::Tensor& h, const at::Tensor& x,
+                                                              const std::optional<at::Tensor>& grad) {
+  auto r = mix_run(h, x, grad, true);
+  if (!grad) std::get<1>(r) = at::empty({0}, h.options());
+  return r;
+}
+
 using MatrixExpOp = c10::TypedOperatorHandle<at::Tensor(const at::Tensor&)>;
 using FrechetOp = c10::TypedOperatorHandle<at::Tensor(const at::Tensor&, const at::Tensor&)>;
 
@@ -203,6 +293,9 @@ TORCH_LIBRARY(flash_hypercons, m) {
   m.def("_frechet(Tensor input, Tensor direction) -> Tensor");
   m.def("_expm_debug(Tensor input, Tensor? direction, int variant) -> (Tensor, Tensor)");
   m.def("_expm_params(Tensor input, Tensor? direction=None) -> (Tensor, Tensor)");
+  m.def("_hc_mix(Tensor h, Tensor x) -> Tensor");
+  m.def("_hc_mix_backward(Tensor h, Tensor x, Tensor grad) -> (Tensor, Tensor)");
+  m.def("_hc_mix_aux(Tensor h, Tensor x, Tensor? grad) -> (Tensor, Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(flash_hypercons, CUDA, m) {
@@ -210,6 +303,9 @@ TORCH_LIBRARY_IMPL(flash_hypercons, CUDA, m) {
   m.impl("_frechet", &flash_hypercons::frechet_hip);
   m.impl("_expm_debug", &flash_hypercons::expm_debug_hip);
   m.impl("_expm_params", &flash_hypercons::expm_params_hip);
+  m.impl("_hc_mix", &flash_hypercons::hc_mix_hip);
+  m.impl("_hc_mix_backward", &flash_hypercons::hc_mix_backward_hip);
+  m.impl("_hc_mix_aux", &flash_hypercons::hc_mix_aux_hip);
 }
 
 TORCH_LIBRARY_IMPL(flash_hypercons, Autograd, m) { m.impl("_matrix_exp", &flash_hypercons::matrix_exp_autograd); }

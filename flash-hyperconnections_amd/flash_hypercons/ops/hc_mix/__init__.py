@@ -1,0 +1,100 @@
+"""Hyper-connection stream mixing with the matrix exponential fused in.
+
+``mix_streams(h, x)`` returns ``matrix_exp(h) @ x`` for ``h`` of shape
+``[B, n, n]`` (the per-token mixing generator) and ``x`` of shape ``[B, n, C]``
+(the n residual streams of each token).  The reference stops at
+``matrix_exp(h)`` (ops/matrix_exp/__init__.py:80-97) and leaves the product to
+the caller; on a gfx950 device with 2 <= n <= 4 and float32 / float16 /
+bfloat16 operands of one dtype this build computes the product in the same
+kernel that computes exp(h), so exp(h) never goes through memory, and the
+backward is one kernel as well (dX = exp(h)^T dY, dE = dY X^T reduced on chip,
+dH = L(h^T, dE)).  Everything else -- other n, CPU tensors, function
+transforms, forward-mode tangents, a backward that builds a graph -- is the
+composition ``matrix_exp(h) @ x`` with this package's ``matrix_exp``.
+"""
+
+import torch
+
+from flash_hypercons import _C  # noqa: F401  (registers the flash_hypercons::* operators)
+from flash_hypercons.ops.matrix_exp import _device_supported, _frechet_differentiable, matrix_exp
+
+_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+
+
+def _fused(h: torch.Tensor, x: torch.Tensor) -> bool:
+    return (
+        isinstance(h, torch.Tensor)
+        and isinstance(x, torch.Tensor)
+        and type(h) in (torch.Tensor, torch.nn.Parameter)
+        and type(x) in (torch.Tensor, torch.nn.Parameter)
+        and not torch._C._are_functorch_transforms_active()
+        and h.device.type == "cuda"
+        and torch.version.hip is not None
+        and x.device == h.device
+        and h.layout == torch.strided
+        and x.layout == torch.strided
+        and h.ndim == 3
+        and x.ndim == 3
+        and h.shape[-1] == h.shape[-2]
+        and 2 <= h.shape[-1] <= 4
+        and x.shape[0] == h.shape[0]
+        and x.shape[1] == h.shape[1]
+        and x.shape[2] >= 1
+        and h.dtype in _DTYPES
+        and x.dtype == h.dtype
+        and torch.autograd.forward_ad.unpack_dual(h).tangent is None
+        and torch.autograd.forward_ad.unpack_dual(x).tangent is None
+        and _device_supported(h.device.index)
+    )
+
+
+@torch.library.register_fake("flash_hypercons::_hc_mix")
+def _hc_mix_fake(h, x):
+    torch._check(h.ndim == 3 and x.ndim == 3)
+    torch._check(x.shape[0] == h.shape[0] and x.shape[1] == h.shape[1])
+    return x.new_empty(x.shape)
+
+
+@torch.library.register_fake("flash_hypercons::_hc_mix_backward")
+def _hc_mix_backward_fake(h, x, grad):
+    torch._check(grad.shape == x.shape)
+    return h.new_empty(h.shape), x.new_empty(x.shape)
+
+
+@torch.library.register_fake("flash_hypercons::_hc_mix_aux")
+def _hc_mix_aux_fake(h, x, grad):
+    second = h.new_empty(h.shape) if grad is not None else h.new_empty((0,))
+    return x.new_empty(x.shape), second, h.new_empty(h.shape, dtype=torch.float32)
+
+
+class _MixStreams(torch.autograd.Function):
+    @staticmethod
+    def forward(h, x):
+        return torch.ops.flash_hypercons._hc_mix(h, x)
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        ctx.save_for_backward(*inputs)
+
+    @staticmethod
+    def backward(ctx, grad):
+        h, x = ctx.saved_tensors
+        if torch.is_grad_enabled():
+            # A backward that builds a graph: the same gradients from differentiable pieces.
+            return _frechet_differentiable(h.mT, grad @ x.mT), matrix_exp(h).mT @ grad
+        dh, dx = torch.ops.flash_hypercons._hc_mix_backward(h, x, grad.contiguous())
+        return dh, dx
+
+
+def mix_streams(h: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """exp(h) @ x per token: h [B, n, n], x [B, n, C] -> [B, n, C] (hyper-connection stream mixing).
+
+    Differentiable in both arguments.  Fused into one HIP kernel per direction for
+    2 <= n <= 4 on gfx950; otherwise composed from ``matrix_exp`` and a batched product.
+    """
+    if _fused(h, x):
+        return _MixStreams.apply(h, x)
+    return matrix_exp(h) @ x
+
+
+__all__ = ["mix_streams"]

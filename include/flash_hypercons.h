@@ -97,6 +97,30 @@ FH_API int fh_expm_params(const void* input, const int64_t input_strides[3], int
                    const int64_t direction_strides[3], int direction_neg, int dtype, int64_t batch, int n,
                    int32_t* params, double* norms, hipStream_t stream);
 
+/* Hyper-connection stream mixing with the exponential fused in:
+ * y[b] = exp(h[b]) x[b] for h [batch, n, n] (any strides, lazy negation) and
+ * x [batch, n, cols], 2 <= n <= 4 streams; y is a contiguous [batch, n, cols]
+ * array of the same dtype.  x's rows must be contiguous and 16-byte aligned,
+ * with cols and x's strides multiples of 16 bytes' worth of elements (4 in
+ * float32, 8 in float16/bfloat16) and each token's rows spanning < 2 GiB.
+ * exp(h[b]) is the same as fh_matrix_exp's (bit for bit) and never goes
+ * to memory; e_out (float32 [batch, n, n], may be NULL) receives a copy.
+ * No counterpart in the reference: its matrix_exp (flash_hypercons/ops/
+ * matrix_exp/__init__.py:80-97) returns exp(h) and the caller multiplies; this
+ * is the consumer fusion of that product.  Allocates nothing. */
+FH_API int fh_hc_mix(const void* h, const int64_t h_strides[3], int h_neg, const void* x, const int64_t x_strides[3],
+              void* y, float* e_out, int dtype, int64_t batch, int n, int64_t cols, hipStream_t stream);
+
+/* Gradients of fh_hc_mix for the upstream gradient grad (same layout rules
+ * as x): dx = exp(h)^T grad (contiguous [batch, n, cols]) and
+ * dh = L(h^T, grad x^T) (contiguous [batch, n, n]), the Frechet derivative
+ * computed as fh_frechet does, from the float32 grad x^T reduced in a fixed
+ * order (de_out, float32 [batch, n, n], may be NULL, receives it).  One kernel;
+ * allocates nothing. */
+FH_API int fh_hc_mix_backward(const void* h, const int64_t h_strides[3], int h_neg, const void* x,
+                       const int64_t x_strides[3], const void* grad, const int64_t grad_strides[3], void* dh,
+                       void* dx, float* de_out, int dtype, int64_t batch, int n, int64_t cols, hipStream_t stream);
+
 /* Message of the last failing call on this thread ("" if none). */
 FH_API const char* fh_last_error(void);
 

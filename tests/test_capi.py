@@ -28,8 +28,8 @@ def load():
 
 def test_headers_declare_entry_points():
     names = declared_functions()
-    assert {"fh_matrix_exp", "fh_frechet", "fh_expm_launch", "fh_expm_params", "fh_last_error",
-            "fh_version"} <= set(names)
+    assert {"fh_matrix_exp", "fh_frechet", "fh_expm_launch", "fh_expm_params", "fh_hc_mix", "fh_hc_mix_backward",
+            "fh_last_error", "fh_version"} <= set(names)
 
 
 @pytest.mark.parametrize("name", declared_functions())
@@ -62,12 +62,52 @@ def test_version_and_validation_without_gpu():
     assert b"direction" in lib.fh_last_error()
 
 
+def test_hc_mix_validation_without_gpu():
+    lib = load()
+    lib.fh_last_error.restype = ctypes.c_char_p
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+    lib.fh_hc_mix.argtypes = [vp, vp, i32, vp, vp, vp, vp, i32, i64, i32, i64, vp]
+    lib.fh_hc_mix_backward.argtypes = [vp, vp, i32, vp, vp, vp, vp, vp, vp, vp, i32, i64, i32, i64, vp]
+    hs = (ctypes.c_int64 * 3)(16, 4, 1)
+    xs = (ctypes.c_int64 * 3)(4 * 64, 64, 1)
+    fake = 1 << 20  # never dereferenced: every call below returns before a HIP call
+    # n outside [2, 4], unknown dtype, C < 1.
+    for n, dtype, cols in ((5, 0, 64), (1, 0, 64), (4, 3, 64), (4, 0, 0)):
+        assert lib.fh_hc_mix(fake, hs, 0, fake, xs, fake, None, dtype, 2, n, cols, None) == 1
+        assert b"2 <= n <= 4" in lib.fh_last_error()
+    # Empty batch: no-op.
+    assert lib.fh_hc_mix(None, hs, 0, None, xs, None, None, 0, 0, 4, 64, None) == 0
+    # Null pointers.
+    assert lib.fh_hc_mix(None, hs, 0, fake, xs, fake, None, 0, 2, 4, 64, None) == 1
+    assert b"null pointer" in lib.fh_last_error()
+    # Rows: C and strides in whole 16-byte vectors, unit column stride, aligned base.
+    bad_rows = (
+        ((ctypes.c_int64 * 3)(4 * 64, 64, 2), fake, 64),
+        ((ctypes.c_int64 * 3)(4 * 64, 66, 1), fake, 64),
+        (xs, fake, 62),
+        (xs, fake + 4, 64),
+        ((ctypes.c_int64 * 3)(4 * 64, -64, 1), fake, 64),
+        ((ctypes.c_int64 * 3)(0, 1 << 29, 1), fake, 64),  # one token spans more than 2 GiB
+    )
+    for strides, ptr, cols in bad_rows:
+        assert lib.fh_hc_mix(fake, hs, 0, ptr, strides, fake, None, 0, 2, 4, cols, None) == 1
+        assert b"16-byte aligned rows" in lib.fh_last_error()
+    # Backward: grad rows follow the same rule; grad and dh must be given.
+    bad = (ctypes.c_int64 * 3)(4 * 64, 64, 2)
+    assert lib.fh_hc_mix_backward(fake, hs, 0, fake, xs, fake, bad, fake, fake, None, 0, 2, 4, 64, None) == 1
+    assert b"16-byte aligned rows" in lib.fh_last_error()
+    assert lib.fh_hc_mix_backward(fake, hs, 0, fake, xs, None, xs, fake, fake, None, 0, 2, 4, 64, None) == 1
+    assert lib.fh_hc_mix_backward(fake, hs, 0, fake, xs, fake, xs, None, fake, None, 0, 2, 4, 64, None) == 1
+    assert b"null grad or dh" in lib.fh_last_error()
+
+
 def test_extension_registers_operators():
     import torch
 
     import flash_hypercons  # noqa: F401
 
-    for name in ("_matrix_exp", "_frechet", "_expm_params", "_expm_debug"):
+    for name in ("_matrix_exp", "_frechet", "_expm_params", "_expm_debug", "_hc_mix", "_hc_mix_backward",
+                 "_hc_mix_aux"):
         assert hasattr(torch.ops.flash_hypercons, name)
     schema = str(torch.ops.flash_hypercons._matrix_exp.default._schema)
     assert schema == "flash_hypercons::_matrix_exp(Tensor input) -> Tensor"

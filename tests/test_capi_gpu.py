@@ -5,7 +5,9 @@ path), passes device pointers, element strides, the negation flag, the dtype
 code and the current HIP stream.  Each launch is compared bit for bit with the
 torch operator on the same logical operands (both run the same kernels), and,
 for n <= 8, with the CPU restatement; squaring counts from ``fh_expm_launch``
-and ``fh_expm_params`` with the restatement's.  Operands: contiguous,
+and ``fh_expm_params`` with the restatement's; ``fh_hc_mix`` and
+``fh_hc_mix_backward`` (exp(h) x and its gradients) with the mixing operators,
+and their exp(h) / dE side outputs with the restatement.  Operands: contiguous,
 transposed views, lazily negated storage and expanded (stride-0) batches.
 """
 
@@ -32,7 +34,10 @@ def _lib():
     lib.fh_frechet.argtypes = [vp, vp, i32, vp, vp, i32, vp, i32, i64, i32, vp]
     lib.fh_expm_launch.argtypes = [vp, vp, i32, vp, vp, i32, vp, i32, i64, i32, i32, vp, vp]
     lib.fh_expm_params.argtypes = [vp, vp, i32, vp, vp, i32, i32, i64, i32, vp, vp, vp]
-    for f in (lib.fh_matrix_exp, lib.fh_frechet, lib.fh_expm_launch, lib.fh_expm_params):
+    lib.fh_hc_mix.argtypes = [vp, vp, i32, vp, vp, vp, vp, i32, i64, i32, i64, vp]
+    lib.fh_hc_mix_backward.argtypes = [vp, vp, i32, vp, vp, vp, vp, vp, vp, vp, i32, i64, i32, i64, vp]
+    for f in (lib.fh_matrix_exp, lib.fh_frechet, lib.fh_expm_launch, lib.fh_expm_params, lib.fh_hc_mix,
+              lib.fh_hc_mix_backward):
         f.restype = ctypes.c_int
     lib.fh_last_error.restype = ctypes.c_char_p
     return lib
@@ -167,3 +172,50 @@ def test_errors_do_not_launch():
     assert rc == 1 and b"2 <= N <= 32" in lib().fh_last_error()
     rc = lib().fh_frechet(x.data_ptr(), strides, 0, None, strides, 0, out.data_ptr(), 0, 2, 4, _stream())
     assert rc == 1 and b"direction must match" in lib().fh_last_error()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("layout", ["contiguous", "transposed", "negated", "expanded"])
+def test_hc_mix_entry_points(layout, dtype):
+    import flash_hypercons  # noqa: F401
+
+    batch, n, cols = 29, 4, 264
+    hv, _ = _values(batch, n, dtype, seed=3 + CODES[dtype])
+    h = Operand(hv, layout)
+    x = torch.randn(batch, n, cols, device="cuda").to(dtype)
+    gy = torch.randn(batch, n, cols, device="cuda").to(dtype)
+    xs, gs = I64x3(*x.stride()), I64x3(*gy.stride())
+    y = torch.empty_like(x)
+    e = torch.empty(batch, n, n, device="cuda")
+    rc = lib().fh_hc_mix(h.ptr, h.strides, h.neg, x.data_ptr(), xs, y.data_ptr(), e.data_ptr(), CODES[dtype], batch,
+                         n, cols, _stream())
+    assert rc == 0, lib().fh_last_error()
+    dh = torch.empty(batch, n, n, dtype=dtype, device="cuda")
+    dx = torch.empty_like(x)
+    de = torch.empty(batch, n, n, device="cuda")
+    rc = lib().fh_hc_mix_backward(h.ptr, h.strides, h.neg, x.data_ptr(), xs, gy.data_ptr(), gs, dh.data_ptr(),
+                                  dx.data_ptr(), de.data_ptr(), CODES[dtype], batch, n, cols, _stream())
+    assert rc == 0, lib().fh_last_error()
+    torch.cuda.synchronize()
+    ops = torch.ops.flash_hypercons
+    assert torch.equal(y, ops._hc_mix(h.logical, x))
+    dh_op, dx_op = ops._hc_mix_backward(h.logical, x, gy)
+    assert torch.equal(dh, dh_op) and torch.equal(dx, dx_op)
+    exp_e, _, _ = oracle.matrix_exp_f32(oracle.tensor_to_f32(h.logical))
+    assert torch.equal(e.cpu(), torch.from_numpy(exp_e))
+    exp_dh, _, _ = oracle.matrix_exp_f32(oracle.tensor_to_f32(h.logical.mT), de.cpu().numpy())
+    assert torch.equal(dh.cpu(), oracle.round_to_dtype(exp_dh, dtype))
+
+
+def test_hc_mix_rejects_unstreamable_rows():
+    x = torch.zeros(2, 4, 10, device="cuda")  # 10 columns: not whole 16-byte vectors
+    h = torch.zeros(2, 4, 4, device="cuda")
+    out = torch.empty_like(x)
+    hs, xs = I64x3(*h.stride()), I64x3(*x.stride())
+    rc = lib().fh_hc_mix(h.data_ptr(), hs, 0, x.data_ptr(), xs, out.data_ptr(), None, 0, 2, 4, 10, _stream())
+    assert rc == 1 and b"multiples of 4 elements" in lib().fh_last_error()
+    x8 = torch.zeros(2, 4, 8, device="cuda")
+    x8s = I64x3(*x8.stride())
+    rc = lib().fh_hc_mix_backward(h.data_ptr(), hs, 0, x8.data_ptr(), x8s, None, x8s, h.data_ptr(), x8.data_ptr(),
+                                  None, 0, 2, 4, 8, _stream())
+    assert rc == 1 and b"null grad" in lib().fh_last_error()

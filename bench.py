@@ -27,7 +27,10 @@ Also reported in the same JSON line:
 * ``configs`` -- configs 3-5 (BF16 N=4 sweep, strided FP32 N=16, FP16 N=32 and
   the same shape in FP32) plus ``p8`` / ``c2s8`` with their own rooflines (HBM
   bytes at 8 TB/s, product flops from each matrix's own squaring count at the
-  FP32 matrix peak);
+  FP32 matrix peak), and ``hc`` -- the fused stream mixing ``fh.mix_streams``
+  (y = exp(h) x, 16,384 tokens x 4 streams x 4,096 columns, BF16) forward and
+  forward + backward, each fused kernel against the HBM roofline, beside the
+  composed ``fh.matrix_exp(h) @ x`` on the same inputs;
 * ``reference_table`` -- the reference's own benchmark (N = 4, 8, 16, 32 at
   B = 65,536 FP32, wall time per direct-API call) beside its published A100
   figures; ``stock_gpu`` -- native torch.linalg.matrix_exp + autograd on this
@@ -243,6 +246,78 @@ def measure_config(name: str, torch, fh, steps: int, warmup: int, trials: int, d
     return out, kept
 
 
+MIX_SHAPE = (16384, 4, 4096)  # tokens, streams, columns
+
+
+def make_mix_inputs(torch, device, shape=MIX_SHAPE, dtype=None):
+    """Seeded inputs of the fused stream mixing: per token an n x n generator h ~ N(0, 0.25^2)
+    (config 2's law) and n residual streams x ~ N(0, 1) of width C; upstream gradient N(0, 1)."""
+    dtype = dtype or torch.bfloat16
+    tokens, n, cols = shape
+    gen = torch.Generator(device=device).manual_seed(0)
+    h = (torch.randn(tokens, n, n, device=device, generator=gen) * 0.25).to(dtype)
+    x = torch.randn(tokens, n, cols, device=device, generator=gen).to(dtype)
+    g = torch.randn(tokens, n, cols, device=device, generator=gen).to(dtype)
+    return h, x, g
+
+
+def measure_mix(torch, fh, steps: int, warmup: int, trials: int, device, keep: bool) -> tuple[dict, dict]:
+    """``fh.mix_streams`` (y = exp(h) x fused, one kernel per direction) against the composed
+    ``fh.matrix_exp(h) @ x`` (exp kernel, then torch's batched product) on the same inputs: the
+    forward alone, and forward + autograd backward of both operands.  HBM roofline of each fused
+    kernel from its algorithmic bytes: forward reads h and x and writes y; backward reads h, x and
+    dy and writes dh and dx."""
+    h, x, g = make_mix_inputs(torch, device)
+    tokens, n, cols = x.shape
+    es = x.element_size()
+    ops = torch.ops.flash_hypercons
+    hr, xr = h.clone().requires_grad_(), x.clone().requires_grad_()
+
+    def fused_step():
+        return torch.autograd.grad(fh.mix_streams(hr, xr), (hr, xr), g)
+
+    def composed_step():
+        return torch.autograd.grad(fh.matrix_exp(hr) @ xr, (hr, xr), g)
+
+    t_fwd = time_trials(torch, lambda: ops._hc_mix(h, x), steps, warmup, trials)
+    t_bwd = time_trials(torch, lambda: ops._hc_mix_backward(h, x, g), steps, warmup, trials)
+    t_step = time_trials(torch, fused_step, steps, warmup, trials)
+    t_cfwd = time_trials(torch, lambda: fh.matrix_exp(h) @ x, steps, warmup, trials)
+    t_cstep = time_trials(torch, composed_step, steps, warmup, trials)
+    bytes_fwd = tokens * (n * n + 2 * n * cols) * es
+    bytes_bwd = tokens * (2 * n * n + 3 * n * cols) * es
+    ms_f, ms_b = t_fwd["median_ms"], t_bwd["median_ms"]
+    out = {
+        "workload": "fh.mix_streams: y = exp(h) @ x per token, h [T, n, n], x [T, n, C]",
+        "shape": [tokens, n, cols],
+        "dtype": str(x.dtype).replace("torch.", ""),
+        "tokens_per_s_fwd_bwd": tokens / (t_step["median_ms"] * 1e-3),
+        "ms_step": t_step["median_ms"],
+        "ms_step_trials": t_step["trials_ms"],
+        "ms_fwd_kernel": ms_f,
+        "ms_bwd_kernel": ms_b,
+        "ms_fwd_trials": t_fwd["trials_ms"],
+        "ms_bwd_trials": t_bwd["trials_ms"],
+        "composed_ms_fwd": t_cfwd["median_ms"],
+        "composed_ms_step": t_cstep["median_ms"],
+        "composed_ms_step_trials": t_cstep["trials_ms"],
+        "speedup_fwd_vs_composed": t_cfwd["median_ms"] / ms_f,
+        "speedup_step_vs_composed": t_cstep["median_ms"] / t_step["median_ms"],
+        "fwd_kernel": {"bound": "hbm", "algorithmic_bytes": bytes_fwd, "achieved_gbs": bytes_fwd / (ms_f * 1e-3) / 1e9,
+                       "frac": bytes_fwd / (ms_f * 1e-3) / 1e9 / HBM_PEAK_GBS},
+        "bwd_kernel": {"bound": "hbm", "algorithmic_bytes": bytes_bwd, "achieved_gbs": bytes_bwd / (ms_b * 1e-3) / 1e9,
+                       "frac": bytes_bwd / (ms_b * 1e-3) / 1e9 / HBM_PEAK_GBS},
+        "roofline_frac_step": (bytes_fwd + bytes_bwd) / (HBM_PEAK_GBS * 1e9) / (t_step["median_ms"] * 1e-3),
+    }
+    kept = {}
+    if keep:
+        y, _, e = ops._hc_mix_aux(h, x, None)
+        dx, dh, de = ops._hc_mix_aux(h, x, g)
+        kept = {"h": h, "x": x, "g": g, "y": y, "e": e, "dx": dx, "dh": dh, "de": de}
+    del hr, xr
+    return out, kept
+
+
 def cold_step(torch, fh, steps: int, warmup: int, trials: int, device, sets: int = 4) -> dict:
     """Config 2's step cycling through `sets` distinct input/gradient sets (each 128 MiB), so the
     working set of consecutive steps exceeds the 256 MB last-level cache."""
@@ -300,7 +375,7 @@ def _cpu_model() -> tuple[str, int | None]:
     return model, (cores * sockets if cores and sockets else None)
 
 
-def cpu_leg(torch, kept: dict) -> dict:
+def cpu_leg(torch, kept: dict, mix_kept: dict | None = None) -> dict:
     """The CPU side of the run, after every GPU timing: the reference's CPU path timed over all of
     config 2, the C restatement timed over the same workload, and the parity block built from the
     restatement's results (the restatement is the checker here, never the thing measured on the
@@ -378,10 +453,21 @@ def cpu_leg(torch, kept: dict) -> dict:
         log(f"[bench] parity {name} ({time.perf_counter() - t0:.1f} s): {json.dumps(parity[name])}")
     failures = {f"{name}.{d}": why for name, rep in parity.items() for d, r in rep.items()
                 if (why := check(r, kept[name]["x"].shape[-1]))}
+    if mix_kept:
+        from tests.mixcheck import check_mix, mix_parity
+
+        t0 = time.perf_counter()
+        k = mix_kept
+        parity["hc"] = mix_parity(k["h"], k["x"], k["g"], k["y"], k["e"], k["dx"], k["dh"], k["de"], threads=threads)
+        log(f"[bench] parity hc ({time.perf_counter() - t0:.1f} s): {json.dumps(parity['hc'])}")
+        if why := check_mix(parity["hc"]):
+            failures["hc"] = why
     result["parity"] = {"pass": not failures, "failures": failures, "configs": parity,
                         "rule": "tests/fullsize.py check(): s == oracle for every matrix; n <= 8 bit-identical "
                         "to the oracle; strict north-star failures <= the oracle's; FP32 mean error <= 1.05x "
-                        "the oracle's; per-matrix excess over the oracle's error under a sanity cap"}
+                        "the oracle's; per-matrix excess over the oracle's error under a sanity cap. hc "
+                        "(tests/mixcheck.py): exp(h) and dh bit-identical to the oracle, y / dx / dE within "
+                        "the FP32 summation bound of the FP64 products, every token"}
     return result
 
 
@@ -495,7 +581,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--trials", type=int, default=5, help="the K timed steps are split into this many trials")
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU leg (CPU baselines and parity)")
-    ap.add_argument("--only", default=None, help="comma list of configs (c2,c3,c4,c5,c5f32,p8,c2s8)")
+    ap.add_argument("--only", default=None, help="comma list of configs (c2,c3,c4,c5,c5f32,p8,c2s8,hc)")
     ap.add_argument("--extras", action="store_true",
                     help="with --only: also run the reference table and the small-batch latency")
     ap.add_argument("--sweep", action="store_true",
@@ -524,10 +610,15 @@ def main() -> int:
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    configs = (args.only or "c2,c3,c4,c5,c5f32,p8,c2s8").split(",")
-    results, kept = {}, {}
+    configs = (args.only or "c2,c3,c4,c5,c5f32,p8,c2s8,hc").split(",")
+    results, kept, mix_kept = {}, {}, None
     for name in configs:
         log(f"[bench] {name} ...")
+        if name == "hc":
+            results[name], mix_kept = measure_mix(torch, fh, args.steps, args.warmup, args.trials, device,
+                                                  keep=not args.skip_cpu)
+            log(f"[bench] {name}: {json.dumps(results[name])}")
+            continue
         results[name], k = measure_config(name, torch, fh, args.steps, args.warmup, args.trials, device,
                                           keep=not args.skip_cpu and name != "c2s8")
         if k:
@@ -600,7 +691,7 @@ def main() -> int:
             line["cold_over_warm"] = cold["ms_step"] / head["ms_step"]
     if not args.skip_cpu:
         log("[bench] cpu leg ...")
-        leg = cpu_leg(torch, kept)
+        leg = cpu_leg(torch, kept, mix_kept)
         line["cpu_baseline"] = leg["cpu_baseline"]
         line["cpu_oracle_port"] = leg["cpu_oracle_port"]
         line["parity"] = leg["parity"]

@@ -6,14 +6,20 @@
 // fuses this; its matrix_exp (ops/matrix_exp/__init__.py:80-97) returns
 // exp(H) to the caller, who multiplies.  Here exp(H_b) never leaves the chip:
 //
-// * A wavefront takes kTokens consecutive tokens.  Lane l computes exp(H) of
-//   token l % kTokens with the per-lane P == 4 code (p4_lane.h, the same
-//   arithmetic as the matrix-exponential kernel, so E is bit-identical to it)
-//   and parks it in the wavefront's LDS.
+// * A wavefront takes a set of kTokens tokens spread over the batch: set k of
+//   S = ceil(B / kTokens) holds tokens k, k + S, k + 2S, ..., so wavefronts
+//   running at the same time stream neighbouring tokens and the rows in flight
+//   form one contiguous region of HBM (consecutive tokens per wavefront put
+//   every concurrent access 8 tokens apart, a power-of-two stride that costs
+//   about 15% of the bandwidth).  Lane l computes exp(H) of the set's token
+//   l % kTokens with the per-lane P == 4 code (p4_lane.h, the same arithmetic
+//   as the matrix-exponential kernel, so E is bit-identical to it) and parks
+//   it in the wavefront's LDS.
 // * The wavefront then streams each token's rows: every lane loads 16 bytes
 //   of each of the n rows per chunk (the whole wavefront covers 1 KB of each
 //   row per chunk, coalesced), multiplies by E read back from LDS (one
 //   broadcast read per token) and stores 16 bytes of each output row.  Rows
+//   are read and written once, with the nontemporal cache hint.  Rows
 //   are addressed through a buffer resource rebased per token in SGPRs, so no
 //   VALU address arithmetic is needed and offsets never exceed one token.
 // * The backward accumulates dE_b = dY_b X_b^T per lane over its columns (in
@@ -96,12 +102,27 @@ __device__ __forceinline__ U32x4 pack(const Vec<T>& v) {
   return w;
 }
 
+// Stream rows with the nontemporal hint (cache-policy bit 1: "nt" on gfx950).
+constexpr int kStreamPolicy = 2;
+
 __device__ __forceinline__ U32x4 load16(__amdgpu_buffer_rsrc_t rs, int32_t voff) {
-  return __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 0, 0);
+  return __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 0, kStreamPolicy);
 }
 
 __device__ __forceinline__ void store16(U32x4 w, __amdgpu_buffer_rsrc_t rs, int32_t voff) {
-  __builtin_amdgcn_raw_buffer_store_b128(w, rs, voff, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b128(w, rs, voff, 0, kStreamPolicy);
+}
+
+// Token set `k` of `sets` = ceil(batch / kTokens): tokens k + i * sets, i < count.
+struct TokenSet {
+  int64_t first, stride;
+  int count;
+  __device__ __forceinline__ int64_t token(int i) const { return first + i * stride; }
+};
+
+__device__ __forceinline__ TokenSet token_set(int64_t k, int64_t sets, int64_t batch) {
+  const int64_t left = (batch - k + sets - 1) / sets;
+  return TokenSet{k, sets, static_cast<int>(left < kTokens ? left : kTokens)};
 }
 
 // exp(H) of token `b` for this lane (valid lanes), NaN for a non-finite H
@@ -124,13 +145,14 @@ __device__ __forceinline__ M4 exp_of_token(const Operand& h, int64_t b, bool val
   return e;
 }
 
-// The wavefront's tokens [t0, t0 + kTokens): lane l holds exp(H) of token
-// t0 + l % kTokens and lanes below kTokens park it in `etile` (16 floats per
-// token); `aux` (optional) receives it in FP32.
+// The wavefront's token set: lane l holds exp(H) of token l % kTokens of the
+// set and lanes below kTokens park it in `etile` (16 floats per token); `aux`
+// (optional) receives it in FP32.
 template <typename T, int N>
-__device__ __forceinline__ void exp_tokens(const HcArgs& a, int64_t t0, int lane, float* etile) {
-  const int64_t b = t0 + (lane & (kTokens - 1));
-  const bool valid = b < a.batch;
+__device__ __forceinline__ void exp_tokens(const HcArgs& a, const TokenSet& ts, int lane, float* etile) {
+  const int slot = lane & (kTokens - 1);
+  const int64_t b = ts.token(slot);
+  const bool valid = slot < ts.count;
   const M4 e = exp_of_token<T, N>(a.h, b, valid);
   if (lane < kTokens) {
 #pragma unroll
@@ -175,15 +197,14 @@ __global__ __launch_bounds__(64 * kWaves) void hc_mix_fwd_kernel(HcArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   float* etile = etile_mem[wave];
-  const int64_t blocks = (a.batch + kTokens - 1) / kTokens;
+  const int64_t sets = (a.batch + kTokens - 1) / kTokens;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kWaves;
   const int64_t span = static_cast<int64_t>(64) * V * kChunks;  // columns per pass
-  for (int64_t blk = static_cast<int64_t>(blockIdx.x) * kWaves + wave; blk < blocks; blk += stride) {
-    const int64_t t0 = blk * kTokens;
-    exp_tokens<T, N>(a, t0, lane, etile);
-    const int ntok = static_cast<int>(a.batch - t0 < kTokens ? a.batch - t0 : kTokens);
-    for (int i = 0; i < ntok; ++i) {
-      const int64_t b = t0 + i;
+  for (int64_t set = static_cast<int64_t>(blockIdx.x) * kWaves + wave; set < sets; set += stride) {
+    const TokenSet ts = token_set(set, sets, a.batch);
+    exp_tokens<T, N>(a, ts, lane, etile);
+    for (int i = 0; i < ts.count; ++i) {
+      const int64_t b = ts.token(i);
       const M4 e = read_token(etile, i);
       const __amdgpu_buffer_rsrc_t xs = rebased<T>(a.x, b * a.xb, ((N - 1) * a.xr + a.cols) * es);
       const __amdgpu_buffer_rsrc_t ys = rebased<T>(a.out, b * N * a.cols, N * a.cols * es);
@@ -261,15 +282,14 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   float* etile = etile_mem[wave];
   float* gtile = gtile_mem[wave];
-  const int64_t blocks = (a.batch + kTokens - 1) / kTokens;
+  const int64_t sets = (a.batch + kTokens - 1) / kTokens;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kWaves;
   const int64_t span = static_cast<int64_t>(64) * V * kChunksBwd;
-  for (int64_t blk = static_cast<int64_t>(blockIdx.x) * kWaves + wave; blk < blocks; blk += stride) {
-    const int64_t t0 = blk * kTokens;
-    exp_tokens<T, N>(a, t0, lane, etile);
-    const int ntok = static_cast<int>(a.batch - t0 < kTokens ? a.batch - t0 : kTokens);
-    for (int i = 0; i < ntok; ++i) {
-      const int64_t b = t0 + i;
+  for (int64_t set = static_cast<int64_t>(blockIdx.x) * kWaves + wave; set < sets; set += stride) {
+    const TokenSet ts = token_set(set, sets, a.batch);
+    exp_tokens<T, N>(a, ts, lane, etile);
+    for (int i = 0; i < ts.count; ++i) {
+      const int64_t b = ts.token(i);
       const M4 e = read_token(etile, i);
       const __amdgpu_buffer_rsrc_t xs = rebased<T>(a.x, b * a.xb, ((N - 1) * a.xr + a.cols) * es);
       const __amdgpu_buffer_rsrc_t gs = rebased<T>(a.gy, b * a.gb, ((N - 1) * a.gr + a.cols) * es);
@@ -321,9 +341,10 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
       if (lane < 16) gtile[16 * i + bitrev4(lane)] = total;
     }
     lds_order();
-    // L(H^T, dE) of token t0 + lane % kTokens.
-    const int64_t b = t0 + (lane & (kTokens - 1));
-    const bool valid = b < a.batch;
+    // L(H^T, dE) of the set's token lane % kTokens.
+    const int slot = lane & (kTokens - 1);
+    const int64_t b = ts.token(slot);
+    const bool valid = slot < ts.count;
     PM<true> cur;
     if (valid) {
       const M4 h = load_elements<T>(a.h, b, N);
@@ -331,7 +352,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
       for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int c = 0; c < 4; ++c) cur.d.v[4 * r + c] = h.v[4 * c + r];
-      cur.u = read_token(gtile, lane & (kTokens - 1));
+      cur.u = read_token(gtile, slot);
     } else {
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
@@ -360,9 +381,9 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
 
 template <typename K>
 hipError_t launch_waves(K kernel, const HcArgs& a, hipStream_t stream) {
-  const int64_t blocks = (a.batch + kTokens - 1) / kTokens;
+  const int64_t sets = (a.batch + kTokens - 1) / kTokens;
   const int64_t resident = resident_blocks(reinterpret_cast<const void*>(kernel), 64 * kWaves);
-  int64_t grid = (blocks + kWaves - 1) / kWaves;
+  int64_t grid = (sets + kWaves - 1) / kWaves;
   if (grid > resident) grid = resident;
   if (grid < 1) grid = 1;
   hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(64 * kWaves), 0, stream, a);

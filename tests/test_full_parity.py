@@ -15,6 +15,11 @@ matrix of the batch and both directions (tests/fullsize.py):
   around the restatement; a real mistake lands orders of magnitude above).
 
 Each config prints its counts, so a run records them.
+
+The fused stream mixing's bench workload (``fh.mix_streams``, 16,384 tokens x
+4 streams x 4,096 columns, BF16) is checked over every token as well
+(tests/mixcheck.py): exp(h) and dh bit-identical to the restatement, y, dx and
+dE within the FP32 summation bound of FP64 products.
 """
 
 import json
@@ -23,7 +28,9 @@ import pytest
 import torch
 
 import flash_hypercons as fh
+import oracle
 from tests.fullsize import check, workload_parity
+from tests.mixcheck import check_mix, mix_parity
 
 pytestmark = pytest.mark.gpu
 
@@ -50,3 +57,19 @@ def test_every_matrix_of_baseline_config(name):
         # The reference's own FP32 arithmetic leaves the strict 1e-5 forward bound on some
         # large-s matrices of this workload; the kernels must not add to them.
         assert report["forward"]["strict_failures_oracle"] > 0
+
+
+def test_every_token_of_the_mixing_workload():
+    import bench
+
+    h, x, g = bench.make_mix_inputs(torch, "cuda")
+    ops = torch.ops.flash_hypercons
+    y, _, e = ops._hc_mix_aux(h, x, None)
+    dx, dh, de = ops._hc_mix_aux(h, x, g)
+    hr, xr = h.clone().requires_grad_(), x.clone().requires_grad_()
+    y2 = fh.mix_streams(hr, xr)
+    dh2, dx2 = torch.autograd.grad(y2, (hr, xr), g)
+    assert torch.equal(y2, y) and torch.equal(dh2, dh) and torch.equal(dx2, dx)
+    report = mix_parity(h, x, g, y, e, dx, dh, de, threads=oracle.default_threads())
+    print(f"[parity] hc {json.dumps(report)}", flush=True)
+    assert not check_mix(report), check_mix(report)

@@ -24,19 +24,17 @@ direction for 2 <= n <= 4.  Checks, on the GPU:
   function transforms) is the composed ``matrix_exp(h) @ x``.
 """
 
-import numpy as np
 import pytest
 import torch
 
 import flash_hypercons as fh
 import oracle
 
+from tests.mixcheck import bound_violations, dE_terms, oracle_exp, oracle_frechet
+
 DTYPES = [torch.float32, torch.float16, torch.bfloat16]
-# Relative half-ulp of the stored result and half the smallest subnormal spacing.
-HALF_ULP = {torch.float32: 0.0, torch.float16: 2.0**-11, torch.bfloat16: 2.0**-8}
-FLOOR = {torch.float32: 2.0**-150, torch.float16: 2.0**-25, torch.bfloat16: 2.0**-134}
-U32 = 2.0**-24
 OPS = torch.ops.flash_hypercons
+THREADS = oracle.default_threads()
 
 
 def _bits(t):
@@ -55,26 +53,11 @@ def _inputs(b, n, c, dtype, scale=0.7, device="cuda"):
 
 
 def _oracle_exp(h):
-    out, _, _ = oracle.matrix_exp_f32(oracle.tensor_to_f32(h), threads=oracle.default_threads())
-    return torch.from_numpy(out)
+    return oracle_exp(h, THREADS)
 
 
 def _oracle_frechet(a, d):
-    out, _, _ = oracle.matrix_exp_f32(oracle.tensor_to_f32(a), oracle.tensor_to_f32(d), threads=oracle.default_threads())
-    return out
-
-
-def bound_violations(actual, ref64, scale64, terms, dtype):
-    """Entries with |actual - ref| > u_out |ref| + terms * 2^-24 (1 + u_out) scale + floor.
-
-    ``scale`` is |A| @ |B| of the product, so the second term bounds a summation
-    of that product with ``terms`` roundings in FP32; u_out is the relative
-    half-ulp of the storage dtype (0 when the result stays FP32).
-    """
-    a = actual.detach().double().cpu()
-    u = HALF_ULP[dtype]
-    bound = u * ref64.abs() + terms * U32 * (1 + u) * scale64 + FLOOR[dtype]
-    return int(((a - ref64).abs() > bound).sum())
+    return oracle_frechet(a, d, THREADS)
 
 
 # --- forward ---------------------------------------------------------------------------------------------
@@ -118,7 +101,7 @@ def _backward_checks(h, x, g, dtype):
     dx, dh, de = OPS._hc_mix_aux(h, x, g)
     e64 = _oracle_exp(h).double()
     x64, g64 = x.double().cpu(), g.double().cpu()
-    assert bound_violations(de, g64 @ x64.mT, g64.abs() @ x64.abs().mT, c // 64 + 24, torch.float32) == 0
+    assert bound_violations(de, g64 @ x64.mT, g64.abs() @ x64.abs().mT, dE_terms(c), torch.float32) == 0
     dh_ref = oracle.round_to_dtype(_oracle_frechet(h.mT, de), dtype)
     assert same_bits(dh.cpu(), dh_ref), "dh differs from the restatement's L(h^T, dE)"
     assert bound_violations(dx, e64.mT @ g64, e64.abs().mT @ g64.abs(), n, dtype) == 0

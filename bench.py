@@ -150,6 +150,12 @@ def time_trials(torch, fn, steps: int, warmup: int, trials: int) -> dict:
             "mean_ms": sum(p * s for p, s in zip(per_call, split_trials(steps, trials))) / steps}
 
 
+def kernel_launches(steps: int, trials: int) -> int:
+    """Launches of a single-kernel loop: at least 25 per trial, so that the queue runs ahead of the
+    host and a trial's time is the kernels' own (its first launch's latency amortised)."""
+    return max(steps, 25 * max(1, trials))
+
+
 def roofline_times(nbytes: float, nflops: float, compute_peak_tflops: float):
     """(bound, seconds) of max(bytes / HBM peak, flops / compute peak)."""
     t_hbm, t_cmp = nbytes / (HBM_PEAK_GBS * 1e9), nflops / (compute_peak_tflops * 1e12)
@@ -170,8 +176,8 @@ def measure_config(name: str, torch, fh, steps: int, warmup: int, trials: int, d
     bwd = torch.ops.flash_hypercons._frechet
     xt = x.detach().mT
     t_step = time_trials(torch, step, steps, warmup, trials)
-    t_fwd = time_trials(torch, lambda: fwd(x), steps, warmup, trials)
-    t_bwd = time_trials(torch, lambda: bwd(xt, g), steps, warmup, trials)
+    t_fwd = time_trials(torch, lambda: fwd(x), kernel_launches(steps, trials), warmup, trials)
+    t_bwd = time_trials(torch, lambda: bwd(xt, g), kernel_launches(steps, trials), warmup, trials)
     ms_step, ms_fwd, ms_bwd = t_step["median_ms"], t_fwd["median_ms"], t_bwd["median_ms"]
 
     # Graph-captured step (launch overhead removed): same kernels, replayed.
@@ -279,8 +285,8 @@ def measure_mix(torch, fh, steps: int, warmup: int, trials: int, device, keep: b
     def composed_step():
         return torch.autograd.grad(fh.matrix_exp(hr) @ xr, (hr, xr), g)
 
-    t_fwd = time_trials(torch, lambda: ops._hc_mix(h, x), steps, warmup, trials)
-    t_bwd = time_trials(torch, lambda: ops._hc_mix_backward(h, x, g), steps, warmup, trials)
+    t_fwd = time_trials(torch, lambda: ops._hc_mix(h, x), kernel_launches(steps, trials), warmup, trials)
+    t_bwd = time_trials(torch, lambda: ops._hc_mix_backward(h, x, g), kernel_launches(steps, trials), warmup, trials)
     t_step = time_trials(torch, fused_step, steps, warmup, trials)
     t_cfwd = time_trials(torch, lambda: fh.matrix_exp(h) @ x, steps, warmup, trials)
     t_cstep = time_trials(torch, composed_step, steps, warmup, trials)
@@ -304,9 +310,11 @@ def measure_mix(torch, fh, steps: int, warmup: int, trials: int, device, keep: b
         "speedup_fwd_vs_composed": t_cfwd["median_ms"] / ms_f,
         "speedup_step_vs_composed": t_cstep["median_ms"] / t_step["median_ms"],
         "fwd_kernel": {"bound": "hbm", "algorithmic_bytes": bytes_fwd, "achieved_gbs": bytes_fwd / (ms_f * 1e-3) / 1e9,
-                       "frac": bytes_fwd / (ms_f * 1e-3) / 1e9 / HBM_PEAK_GBS},
+                       "frac": bytes_fwd / (ms_f * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                       "traffic": profiled_traffic("hc_mix_fwd_bf16_n4", "hc_mix_hbm_traffic.md")},
         "bwd_kernel": {"bound": "hbm", "algorithmic_bytes": bytes_bwd, "achieved_gbs": bytes_bwd / (ms_b * 1e-3) / 1e9,
-                       "frac": bytes_bwd / (ms_b * 1e-3) / 1e9 / HBM_PEAK_GBS},
+                       "frac": bytes_bwd / (ms_b * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                       "traffic": profiled_traffic("hc_mix_bwd_bf16_n4", "hc_mix_hbm_traffic.md")},
         "roofline_frac_step": (bytes_fwd + bytes_bwd) / (HBM_PEAK_GBS * 1e9) / (t_step["median_ms"] * 1e-3),
     }
     kept = {}
@@ -344,9 +352,9 @@ def cold_step(torch, fh, steps: int, warmup: int, trials: int, device, sets: int
             "ms_step_trials": t["trials_ms"], "matrices_per_s_fwd_bwd": b / (t["median_ms"] * 1e-3)}
 
 
-def profiled_traffic(key: str):
+def profiled_traffic(key: str, summary: str = "expm_p4_c2_hbm_traffic.md"):
     """HBM bytes per launch of a kernel from a committed rocprofv3 counter summary (or None)."""
-    path = ROOT / "profiles" / "expm_p4_c2_hbm_traffic.md"
+    path = ROOT / "profiles" / summary
     try:
         for line in path.read_text().splitlines():
             if line.startswith("traffic_bytes_per_launch " + key + " = "):

@@ -8,6 +8,9 @@ Produces, inside ``flash_hypercons/``:
   ``flash_hypercons::*`` operators and calls the C ABI (host-only C++).
 
 Run ``python flash-hyperconnections_amd/build.py`` (or ``__graft_entry__.build()``).
+``pip install`` (setup.py at the repository root) calls ``build(out_dir=...,
+obj_dir=...)`` to place both libraries in the wheel's package directory
+instead of the source tree.
 """
 
 from __future__ import annotations
@@ -73,24 +76,25 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
 
 
-def _compile(src: str) -> Path:
-    obj = OBJ / (src + ".o")
+def _compile(src: str, obj_dir: Path = OBJ) -> Path:
+    obj = obj_dir / (src + ".o")
     _run([HIPCC, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
     return obj
 
 
-def build_library(jobs: int = 8) -> Path:
-    OBJ.mkdir(exist_ok=True)
+def build_library(jobs: int = 8, out_dir: Path = PKG, obj_dir: Path = OBJ) -> Path:
+    obj_dir.mkdir(parents=True, exist_ok=True)
+    out_dir.mkdir(parents=True, exist_ok=True)
     with ThreadPoolExecutor(max_workers=jobs) as pool:
-        objs = list(pool.map(_compile, KERNEL_SOURCES))
-    target = PKG / LIB_NAME
+        objs = list(pool.map(lambda src: _compile(src, obj_dir), KERNEL_SOURCES))
+    target = out_dir / LIB_NAME
     tmp = target.with_suffix(".so.tmp")
     _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(tmp)])
     os.replace(tmp, target)
     return target
 
 
-def build_extension() -> Path:
+def build_extension(out_dir: Path = PKG, obj_dir: Path = OBJ) -> Path:
     import torch
     from torch.utils.cpp_extension import include_paths, library_paths
 
@@ -105,15 +109,15 @@ def build_extension() -> Path:
         f"-I{ROCM / 'include'}",
         f"-I{INCLUDE}",
     ]
-    OBJ.mkdir(exist_ok=True)
-    obj = OBJ / "register.o"
+    obj_dir.mkdir(parents=True, exist_ok=True)
+    obj = obj_dir / "register.o"
     cxx = shutil.which("g++") or "g++"
     _run([cxx, *flags, "-c", str(CSRC / "register.cpp"), "-o", str(obj)])
-    target = PKG / "_C.so"
+    target = out_dir / "_C.so"
     tmp = target.with_suffix(".so.tmp")
     _run([
         cxx, "-shared", str(obj), "-o", str(tmp),
-        f"-L{PKG}", "-l:" + LIB_NAME,
+        f"-L{out_dir}", "-l:" + LIB_NAME,
         f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-ltorch_python",
         f"-L{ROCM / 'lib'}", "-lamdhip64",
         "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}", f"-Wl,-rpath,{ROCM / 'lib'}",
@@ -122,9 +126,9 @@ def build_extension() -> Path:
     return target
 
 
-def build(jobs: int = 8) -> list[Path]:
-    lib = build_library(jobs)
-    ext = build_extension()
+def build(jobs: int = 8, out_dir: Path = PKG, obj_dir: Path = OBJ) -> list[Path]:
+    lib = build_library(jobs, Path(out_dir), Path(obj_dir))
+    ext = build_extension(Path(out_dir), Path(obj_dir))
     return [lib, ext]
 
 

@@ -6,18 +6,22 @@ import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
 PKG_DIR = ROOT / "flash-hyperconnections_amd"
-for path in (str(PKG_DIR), str(ROOT)):
+# FH_TEST_INSTALLED=1: test the flash_hypercons found on sys.path (e.g. a
+# `pip install --target DIR .` copy on PYTHONPATH) instead of the source tree.
+INSTALLED = os.environ.get("FH_TEST_INSTALLED", "") not in ("", "0")
+for path in ((str(ROOT),) if INSTALLED else (str(PKG_DIR), str(ROOT))):
     if path not in sys.path:
         sys.path.insert(0, path)
 
 
 def _ensure_built():
     """Build the extension and the oracle once if this checkout has none (CPU container)."""
-    sys.path.insert(0, str(PKG_DIR))
-    import build as fh_build  # flash-hyperconnections_amd/build.py
+    if not INSTALLED:
+        sys.path.insert(0, str(PKG_DIR))
+        import build as fh_build  # flash-hyperconnections_amd/build.py
 
-    if not fh_build.built():
-        fh_build.build()
+        if not fh_build.built():
+            fh_build.build()
     import oracle
 
     if not oracle.LIB_PATH.exists():

@@ -10,8 +10,10 @@ from pathlib import Path
 
 import pytest
 
+import flash_hypercons
+
 ROOT = Path(__file__).resolve().parents[1]
-LIB = ROOT / "flash-hyperconnections_amd" / "flash_hypercons" / "libflash_hypercons_hip.so"
+LIB = Path(flash_hypercons.__file__).resolve().parent / "libflash_hypercons_hip.so"
 
 
 def declared_functions():
@@ -113,3 +115,16 @@ def test_extension_registers_operators():
     assert schema == "flash_hypercons::_matrix_exp(Tensor input) -> Tensor"
     schema = str(torch.ops.flash_hypercons._frechet.default._schema)
     assert schema == "flash_hypercons::_frechet(Tensor input, Tensor direction) -> Tensor"
+
+
+def test_package_under_test():
+    """The package these tests import: the source tree, or with FH_TEST_INSTALLED set, an
+    installed copy (``pip install --no-build-isolation --target DIR .``) that carries both
+    libraries."""
+    import os
+
+    pkg = Path(flash_hypercons.__file__).resolve().parent
+    in_tree = pkg == (ROOT / "flash-hyperconnections_amd" / "flash_hypercons").resolve()
+    assert in_tree != (os.environ.get("FH_TEST_INSTALLED", "") not in ("", "0"))
+    assert (pkg / "libflash_hypercons_hip.so").is_file() and (pkg / "_C.so").is_file()
+    assert Path(flash_hypercons._C.__file__).resolve().parent == pkg

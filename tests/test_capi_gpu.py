@@ -17,12 +17,13 @@ from pathlib import Path
 import pytest
 import torch
 
+import flash_hypercons
 import oracle
 
 pytestmark = pytest.mark.gpu
 
 ROOT = Path(__file__).resolve().parents[1]
-LIB_PATH = ROOT / "flash-hyperconnections_amd" / "flash_hypercons" / "libflash_hypercons_hip.so"
+LIB_PATH = Path(flash_hypercons.__file__).resolve().parent / "libflash_hypercons_hip.so"
 CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 I64x3 = ctypes.c_int64 * 3
 

@@ -646,7 +646,9 @@ def main() -> int:
         if args.sweep:
             table = reference_table(torch, fh, device, batches=(1, 128, 1024, 65536), dtypes=("f32", "f16", "bf16"))
         else:
-            table = reference_table(torch, fh, device)
+            # Longer trials than the reference's 10 calls: at N <= 8 a call is host-bound and 10
+            # calls leave the median at the mercy of one slow launch.
+            table = reference_table(torch, fh, device, repeat=40, trials=5)
         for row in table["rows"]:
             log(f"[bench] reference table: n={row['n']:2} B={row['batch']:6} {row['dtype']:4} {row['mode']:16} "
                 f"{row['median_us']:9.1f} us (stock GPU {row['stock_gpu_us']:9.1f} us)")

@@ -64,6 +64,8 @@ def lib():
         _lib.fho_f32_to_bf16.argtypes = [f32p, ctypes.POINTER(ctypes.c_uint16), ctypes.c_int64]
         _lib.fho_f32_to_bf16.restype = None
         _lib.fho_coefficients.argtypes = []
+        _lib.fho_set_combine_contraction.argtypes = [ctypes.c_int]
+        _lib.fho_set_combine_contraction.restype = None
         _lib.fho_coefficients.restype = f32p
     return _lib
 
@@ -198,6 +200,12 @@ def _torch():
     return torch
 
 
+def set_combine_contraction(diag_first: bool) -> None:
+    """Test knob: contract each combine's first two terms as fmaf(c0, I, c1*A) (True) instead of
+    the restatement's fmaf(c1, A, c0*I) (False, the default).  Global; not for concurrent use."""
+    lib().fho_set_combine_contraction(1 if diag_first else 0)
+
+
 def tensor_to_f32(t) -> np.ndarray:
     """Exact FP32 copy of a (possibly strided / negated / low-precision) tensor."""
     torch = _torch()
@@ -245,7 +253,7 @@ def torch_params(x, g=None, threads: int = 1):
 __all__ = [
     "THETA18", "DEGREE", "build", "matrix_exp_f32", "params_f32", "norm1", "squarings", "padded_size",
     "coefficients", "f32_to_bf16_bits", "tensor_to_f32", "round_to_dtype", "torch_matrix_exp",
-    "torch_frechet", "torch_params", "default_threads",
+    "torch_frechet", "torch_params", "default_threads", "set_combine_contraction",
 ]
 
 if os.environ.get("FHO_BUILD_ON_IMPORT"):

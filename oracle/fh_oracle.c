@@ -127,6 +127,16 @@ static void add(const Tile* a, const Tile* b, Tile* c, int P, int pair) {
   }
 }
 
+/* Which way the first two terms of a combine contract.  0 (the restatement):
+ * fmaf(c1, A, c0*I), one rounding.  1: fmaf(c0, I, c1*A), the other form a
+ * compiler may choose for the same C expression; it rounds c1*A first, which
+ * changes only diagonal entries of D.  Not observable without the reference
+ * build, so tests use 1 to bound how far the choice could move results.  Set
+ * it before a computation, never during one. */
+static int g_contract_diag_first = 0;
+
+void fho_set_combine_contraction(int diag_first) { g_contract_diag_first = diag_first != 0; }
+
 /* B = c0*I + c1*A + c2*A^2 + c3*A^3 + c6*A^6; the identity goes to D only
  * (MatrixExpSmall.cuh:66-81). */
 static void combine(const Tile* a, const Tile* a2, const Tile* a3, const Tile* a6, const float* c,
@@ -135,7 +145,11 @@ static void combine(const Tile* a, const Tile* a2, const Tile* a3, const Tile* a
     for (int j = 0; j < P; ++j) {
       const int e = i * P + j;
       float t = c[0] * (float)(i == j);
-      t = fmaf(c[1], a->d[e], t);
+      if (g_contract_diag_first && c[1] != 0.f) {
+        t = fmaf(c[0], (float)(i == j), c[1] * a->d[e]);
+      } else {
+        t = fmaf(c[1], a->d[e], t);
+      }
       t = fmaf(c[2], a2->d[e], t);
       t = fmaf(c[3], a3->d[e], t);
       t = fmaf(c[4], a6->d[e], t);

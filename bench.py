@@ -326,6 +326,36 @@ def measure_mix(torch, fh, steps: int, warmup: int, trials: int, device, keep: b
     return out, kept
 
 
+def mix_sweep(torch, fh, device, steps: int = 20, warmup: int = 3, trials: int = 5) -> list:
+    """Fused ``fh.mix_streams`` against the composed ``fh.matrix_exp(h) @ x`` over stream counts,
+    widths and dtypes (forward and forward + backward, HIP-event medians)."""
+    rows = []
+    for dtype in (torch.bfloat16, torch.float32):
+        for n in (2, 3, 4):
+            for cols in (256, 1024, 4096, 7168):
+                if dtype == torch.float32 and cols != 4096:
+                    continue
+                tokens = 16384
+                h, x, g = make_mix_inputs(torch, device, shape=(tokens, n, cols), dtype=dtype)
+                hr, xr = h.clone().requires_grad_(), x.clone().requires_grad_()
+                fused_f = time_trials(torch, lambda: fh.mix_streams(h, x), steps, warmup, trials)["median_ms"]
+                comp_f = time_trials(torch, lambda: fh.matrix_exp(h) @ x, steps, warmup, trials)["median_ms"]
+                fused_s = time_trials(torch, lambda: torch.autograd.grad(fh.mix_streams(hr, xr), (hr, xr), g), steps,
+                                      warmup, trials)["median_ms"]
+                comp_s = time_trials(torch, lambda: torch.autograd.grad(fh.matrix_exp(hr) @ xr, (hr, xr), g), steps,
+                                     warmup, trials)["median_ms"]
+                es = x.element_size()
+                fwd_bytes = tokens * (n * n + 2 * n * cols) * es
+                rows.append({"tokens": tokens, "n": n, "cols": cols, "dtype": str(dtype).replace("torch.", ""),
+                             "fused_fwd_ms": fused_f, "composed_fwd_ms": comp_f, "fused_step_ms": fused_s,
+                             "composed_step_ms": comp_s, "fused_fwd_gbs": fwd_bytes / (fused_f * 1e-3) / 1e9,
+                             "step_speedup": comp_s / fused_s})
+                log(f"[bench] mix sweep n={n} C={cols} {rows[-1]['dtype']}: fused {fused_f * 1e3:.1f} / "
+                    f"{fused_s * 1e3:.1f} us, composed {comp_f * 1e3:.1f} / {comp_s * 1e3:.1f} us")
+                del h, x, g, hr, xr
+    return rows
+
+
 def cold_step(torch, fh, steps: int, warmup: int, trials: int, device, sets: int = 4) -> dict:
     """Config 2's step cycling through `sets` distinct input/gradient sets (each 128 MiB), so the
     working set of consecutive steps exceeds the 256 MB last-level cache."""
@@ -593,7 +623,8 @@ def main() -> int:
     ap.add_argument("--extras", action="store_true",
                     help="with --only: also run the reference table and the small-batch latency")
     ap.add_argument("--sweep", action="store_true",
-                    help="reference table over B in {1,128,1024,65536} x {f32,f16,bf16} (the reference's sweep)")
+                    help="reference table over B in {1,128,1024,65536} x {f32,f16,bf16} (the reference's sweep), "
+                    "and fused vs composed stream mixing over n and C")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one device copy of exactly 64 MiB (profiler counter calibration)")
     args = ap.parse_args()
@@ -639,7 +670,7 @@ def main() -> int:
         log("[bench] cold c2 step ...")
         cold = cold_step(torch, fh, args.steps, args.warmup, args.trials, device)
         log(f"[bench] cold c2 step: {json.dumps(cold)}")
-    table = latency = None
+    table = latency = mix_rows = None
     if args.only is None or args.extras or args.sweep:
         # Not part of --only runs, so that a profile of one config holds only its own launches.
         log("[bench] reference table ...")
@@ -652,6 +683,9 @@ def main() -> int:
         for row in table["rows"]:
             log(f"[bench] reference table: n={row['n']:2} B={row['batch']:6} {row['dtype']:4} {row['mode']:16} "
                 f"{row['median_us']:9.1f} us (stock GPU {row['stock_gpu_us']:9.1f} us)")
+        if args.sweep:
+            log("[bench] stream-mixing sweep ...")
+            mix_rows = mix_sweep(torch, fh, device)
         log("[bench] small-batch latency ...")
         latency = small_batch_latency(torch, fh, device)
         log(f"[bench] small-batch latency: {json.dumps(latency)}")
@@ -708,6 +742,8 @@ def main() -> int:
     if latency is not None:
         line["small_batch_latency"] = latency
         line["reference_table"] = table
+    if mix_rows is not None:
+        line["mix_sweep"] = mix_rows
     line["configs"] = results
     print(json.dumps(line), flush=True)
     return 0

@@ -379,10 +379,13 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
   }
 }
 
-template <typename K>
-hipError_t launch_waves(K kernel, const HcArgs& a, hipStream_t stream) {
+// Grid: one wavefront per token set up to what the device keeps resident
+// (counted once per kernel; the wavefronts stride over the rest).
+template <typename T, int N, bool Backward>
+hipError_t launch_one(const HcArgs& a, hipStream_t stream) {
+  const auto kernel = Backward ? hc_mix_bwd_kernel<T, N> : hc_mix_fwd_kernel<T, N>;
+  static const int64_t resident = resident_blocks(reinterpret_cast<const void*>(kernel), 64 * kWaves);
   const int64_t sets = (a.batch + kTokens - 1) / kTokens;
-  const int64_t resident = resident_blocks(reinterpret_cast<const void*>(kernel), 64 * kWaves);
   int64_t grid = (sets + kWaves - 1) / kWaves;
   if (grid > resident) grid = resident;
   if (grid < 1) grid = 1;
@@ -394,11 +397,11 @@ template <typename T>
 hipError_t launch_t(const HcArgs& a, bool backward, hipStream_t stream) {
   switch (a.n) {
     case 2:
-      return backward ? launch_waves(hc_mix_bwd_kernel<T, 2>, a, stream) : launch_waves(hc_mix_fwd_kernel<T, 2>, a, stream);
+      return backward ? launch_one<T, 2, true>(a, stream) : launch_one<T, 2, false>(a, stream);
     case 3:
-      return backward ? launch_waves(hc_mix_bwd_kernel<T, 3>, a, stream) : launch_waves(hc_mix_fwd_kernel<T, 3>, a, stream);
+      return backward ? launch_one<T, 3, true>(a, stream) : launch_one<T, 3, false>(a, stream);
     default:
-      return backward ? launch_waves(hc_mix_bwd_kernel<T, 4>, a, stream) : launch_waves(hc_mix_fwd_kernel<T, 4>, a, stream);
+      return backward ? launch_one<T, 4, true>(a, stream) : launch_one<T, 4, false>(a, stream);
   }
 }
 

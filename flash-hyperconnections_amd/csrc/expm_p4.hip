@@ -299,6 +299,126 @@ __global__ __launch_bounds__(64 * kP4Waves) __attribute__((amdgpu_waves_per_eu(P
   if (group == full && static_cast<int64_t>(full) * 64 < args.batch) expm_group_elements<T, Pair>(args, group, lane);
 }
 
+// ---- dense operands: groups loaded straight into LDS ------------------------
+//
+// For dense operands the groups go from HBM to the wavefront's LDS with
+// buffer-to-LDS loads, no registers involved, a group ahead in a two-slot
+// ring.  Load instruction c of a group has lane l fetch tuple C l + c of the
+// 64-matrix block, so that it writes LDS row c with matrix l's tuple c at byte
+// 16 l: the padded, conflict-free layout each lane reads its own matrix from.
+// A slot is reused for the group's staged results once its inputs are read.
+
+// Buffer-to-LDS load of 16 bytes per lane: lane l's bytes land at LDS byte
+// address lds_addr + 16 l.  Written as assembly so that the compiler's wait
+// insertion does not make every LDS read wait for these loads (it cannot tell
+// the two slots apart); wait_vm<N>() orders them instead.  `rsrc` is the buffer
+// resource as four words.
+__device__ __forceinline__ void lds_load16(U32x4 rsrc, uint32_t lds_addr, int32_t voff, int32_t soff) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" : : "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds_addr)
+               : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
+}
+
+// Resource words of make_rsrc(base, 0x7FFFFFFF): base address, stride 0,
+// num_records, and the same fourth word.
+__device__ __forceinline__ U32x4 rsrc_words(const void* base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return U32x4{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32) & 0xFFFFu, 0x7FFFFFFFu, 0x00020000u};
+}
+
+// s_waitcnt vmcnt(N): at most N vector memory operations of this wavefront
+// outstanding.  Loads complete in issue order, so this waits for every load
+// issued before the last N loads.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 16, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
+
+// One operand's group block into LDS rows c * 1040 (the dense_to_lane layout).
+template <typename T>
+__device__ __forceinline__ void load_group_to_lds(U32x4 rs, uint32_t lds_addr, int32_t group_bytes, int lane) {
+  constexpr int C = Raw<T>::C;
+#pragma unroll
+  for (int c = 0; c < C; ++c) lds_load16(rs, lds_addr + c * kDenseRowBytes, 16 * C * lane, group_bytes + 16 * c);
+}
+
+template <typename T>
+__device__ __forceinline__ Raw<T> read_lane_tuples(const char* area, int lane) {
+  Raw<T> r;
+#pragma unroll
+  for (int c = 0; c < Raw<T>::C; ++c) r.q[c] = *reinterpret_cast<const uint4*>(area + c * kDenseRowBytes + 16 * lane);
+  return r;
+}
+
+template <typename T, bool Pair>
+struct DmaSlot {
+  static constexpr int kArea = Raw<T>::C * kDenseRowBytes;
+  static constexpr int kIn = (Pair ? 2 : 1) * kArea;
+  static constexpr int kStage = 64 * kStageStride * 4;
+  static constexpr int kBytes = kIn > kStage ? kIn : kStage;  // inputs, then the staged results
+};
+
+// Persistent kernel over the full groups of a batch whose operands are all
+// dense (n == 4).
+template <typename T, bool Pair, int XL, int GL>
+__global__ __launch_bounds__(64 * kP4Waves) __attribute__((amdgpu_waves_per_eu(Pair ? 2 : 4, 8))) void expm_p4_dma_kernel(
+    ExpmArgs args) {
+  using Slot = DmaSlot<T, Pair>;
+  constexpr int es = static_cast<int>(sizeof(typename T::storage));
+  constexpr int kLoads = Raw<T>::C * (Pair ? 2 : 1);  // load instructions per group
+  __shared__ __attribute__((aligned(16))) char tile_mem[kP4Waves][2][Slot::kBytes];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // Groups fit in 32 bits: the host takes this kernel only for operands below 2 GiB.
+  const int32_t full = static_cast<int32_t>(args.batch / 64);
+  const int32_t stride = static_cast<int32_t>(gridDim.x) * kP4Waves;
+  int32_t group = static_cast<int32_t>(blockIdx.x) * kP4Waves + wave;
+  const U32x4 xs = rsrc_words(args.x.data);
+  const U32x4 gs = rsrc_words(Pair ? args.g.data : args.x.data);
+  const __amdgpu_buffer_rsrc_t out_rs = make_rsrc(args.out, 0x7FFFFFFFu);
+  constexpr int32_t kGroupBytes = 64 * 16 * es;
+  auto issue = [&](int32_t g, char* slot) {
+    const uint32_t a = lds_address(slot);
+    load_group_to_lds<T>(xs, a, g * kGroupBytes, lane);
+    if constexpr (Pair) load_group_to_lds<T>(gs, a + Slot::kArea, g * kGroupBytes, lane);
+  };
+  int which = 0;
+  if (group < full) issue(group, tile_mem[wave][0]);
+  for (; group < full; group += stride) {
+    char* slot = tile_mem[wave][which];
+    // The next group's loads go to the other slot (its results were read out
+    // for the stores of the previous round); then wait for this group's.
+    if (group + stride < full) {
+      issue(group + stride, tile_mem[wave][which ^ 1]);
+      wait_vm<kLoads>();
+    } else {
+      wait_vm<0>();
+    }
+    lds_order();
+    PM<Pair> cur;
+    cur.d = decode<T, XL>(read_lane_tuples<T>(slot, lane));
+    if constexpr (Pair) cur.u = decode<T, GL>(read_lane_tuples<T>(slot + Slot::kArea, lane));
+    lds_order();  // inputs read before the staged results overwrite the slot
+    float* stage = reinterpret_cast<float*>(slot);
+    const int s = expm_lane<Pair>(cur, args.x.sign, args.g.sign, [&](const M4& out) { stage_lane(stage, lane, out); });
+    if (s < 0) {  // rare: overwrite the staged block with NaN
+      M4 nan;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) nan.v[e] = __builtin_nanf("");
+      stage_lane(stage, lane, nan);
+    }
+    store_group<T>(out_rs, group * kGroupBytes, lane, stage);
+    if (args.s_out) args.s_out[static_cast<int64_t>(group) * 64 + lane] = s;
+    which ^= 1;
+  }
+  // The partial last group, if any, belongs to the wavefront whose walk reaches it.
+  if (group == full && static_cast<int64_t>(full) * 64 < args.batch) expm_group_elements<T, Pair>(args, group, lane);
+}
+
 // Every group of an element-class batch (n < 4 or strides no vector class
 // fits): per-element loads and stores.
 template <typename T, bool Pair>
@@ -332,9 +452,18 @@ hipError_t launch_vec(const ExpmArgs& args, hipStream_t stream) {
 }
 
 template <typename T, bool Pair, int XL, int GL>
+hipError_t launch_dma(const ExpmArgs& args, hipStream_t stream) {
+  static const int64_t resident =
+      resident_blocks(reinterpret_cast<const void*>(&expm_p4_dma_kernel<T, Pair, XL, GL>), 64 * kP4Waves);
+  const int64_t groups = args.batch / 64 + (args.batch % 64 != 0);
+  return launch_persistent(expm_p4_dma_kernel<T, Pair, XL, GL>, groups, args, stream, resident);
+}
+
+template <typename T, bool Pair, int XL, int GL>
 hipError_t launch_vec_dense(const ExpmArgs& args, hipStream_t stream) {
   const bool xd = args.x.dense != 0;
   const bool gd = Pair && args.g.dense != 0;
+  if (xd && (!Pair || gd)) return launch_dma<T, Pair, XL, GL>(args, stream);
   if (xd) {
     if constexpr (Pair) {
       return gd ? launch_vec<T, Pair, XL, GL, true, true>(args, stream)

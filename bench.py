@@ -327,11 +327,12 @@ def measure_mix(torch, fh, steps: int, warmup: int, trials: int, device, keep: b
 
 
 def mix_sweep(torch, fh, device, steps: int = 20, warmup: int = 3, trials: int = 5) -> list:
-    """Fused ``fh.mix_streams`` against the composed ``fh.matrix_exp(h) @ x`` over stream counts,
-    widths and dtypes (forward and forward + backward, HIP-event medians)."""
+    """``fh.mix_streams`` (fused for n <= 4, exp(h) then one streaming kernel per direction for
+    5 <= n <= 8) against the composed ``fh.matrix_exp(h) @ x`` over stream counts, widths and
+    dtypes (forward and forward + backward, HIP-event medians)."""
     rows = []
     for dtype in (torch.bfloat16, torch.float32):
-        for n in (2, 3, 4):
+        for n in (2, 3, 4, 6, 8):
             for cols in (256, 1024, 4096, 7168):
                 if dtype == torch.float32 and cols != 4096:
                     continue
@@ -347,6 +348,7 @@ def mix_sweep(torch, fh, device, steps: int = 20, warmup: int = 3, trials: int =
                 es = x.element_size()
                 fwd_bytes = tokens * (n * n + 2 * n * cols) * es
                 rows.append({"tokens": tokens, "n": n, "cols": cols, "dtype": str(dtype).replace("torch.", ""),
+                             "path": "fused" if n <= 4 else "exp + apply",
                              "fused_fwd_ms": fused_f, "composed_fwd_ms": comp_f, "fused_step_ms": fused_s,
                              "composed_step_ms": comp_s, "fused_fwd_gbs": fwd_bytes / (fused_f * 1e-3) / 1e9,
                              "step_speedup": comp_s / fused_s})

@@ -118,27 +118,52 @@ int launch(const void* input, const int64_t input_strides[3], int input_neg, con
 // Operands of the fused stream mixing: H any strides; X (and dY) [B, n, C]
 // with contiguous, 16-byte aligned rows of a whole number of 16-byte vectors,
 // each token's rows spanning less than 2 GiB.
+// Rows of a streamed operand ([B, n, C], unit column stride): 16-byte aligned,
+// strides and C whole 16-byte vectors, each token's rows spanning < 2 GiB.
+bool stream_rows_ok(const void* p, const int64_t* st, int n, int64_t cols, int dtype) {
+  constexpr int64_t kSpan = int64_t{1} << 31;  // bytes one token's rows may span (32-bit buffer offsets)
+  const int64_t es = element_size(dtype);
+  const int64_t v = 16 / es;
+  return st != nullptr && aligned(p, 16) && st[2] == 1 && st[0] >= 0 && st[1] >= 0 && st[0] % v == 0 &&
+         st[1] % v == 0 && cols % v == 0 && st[1] < kSpan && cols < kSpan && ((n - 1) * st[1] + cols) * es < kSpan;
+}
+
+bool known_dtype(int dtype) { return dtype == FH_DTYPE_F32 || dtype == FH_DTYPE_BF16 || dtype == FH_DTYPE_F16; }
+
+std::string rows_message(const char* op, int dtype) {
+  return std::string(op) + ": X and dY need contiguous, 16-byte aligned rows whose length C and strides are multiples of " +
+         std::to_string(16 / element_size(dtype)) + " elements";
+}
+
 int validate_hc(const void* h, const int64_t* hs, const void* x, const int64_t* xs, const void* g, const int64_t* gs,
                 const void* out, int dtype, int64_t batch, int n, int64_t cols) {
-  if (n < 2 || n > 4 || (dtype != FH_DTYPE_F32 && dtype != FH_DTYPE_BF16 && dtype != FH_DTYPE_F16) || batch < 0 ||
-      cols < 1)
+  if (n < 2 || n > 4 || !known_dtype(dtype) || batch < 0 || cols < 1)
     return fail(FH_ERR_INVALID_ARGUMENT,
                 "hc_mix: expected H [B, n, n] and X [B, n, C] with 2 <= n <= 4, C >= 1, in float32, float16, or "
                 "bfloat16");
   if (batch == 0) return FH_OK;
   if (h == nullptr || hs == nullptr || x == nullptr || xs == nullptr || out == nullptr)
     return fail(FH_ERR_INVALID_ARGUMENT, "hc_mix: null pointer");
-  const int64_t es = element_size(dtype);
-  const int64_t v = 16 / es;
-  auto rows_ok = [&](const void* p, const int64_t* st) {
-    constexpr int64_t kSpan = int64_t{1} << 31;  // bytes one token's rows may span (32-bit buffer offsets)
-    return aligned(p, 16) && st[2] == 1 && st[0] >= 0 && st[1] >= 0 && st[0] % v == 0 && st[1] % v == 0 &&
-           cols % v == 0 && st[1] < kSpan && cols < kSpan && ((n - 1) * st[1] + cols) * es < kSpan;
-  };
-  if (!rows_ok(x, xs) || (g != nullptr && (gs == nullptr || !rows_ok(g, gs))) || !aligned(out, 16))
+  if (!stream_rows_ok(x, xs, n, cols, dtype) || (g != nullptr && !stream_rows_ok(g, gs, n, cols, dtype)) ||
+      !aligned(out, 16))
+    return fail(FH_ERR_INVALID_ARGUMENT, rows_message("hc_mix", dtype));
+  return FH_OK;
+}
+
+// The apply entry points (5 <= n <= 8): E is FP32 [batch, n, n], contiguous.
+int validate_apply(const float* e, const void* x, const int64_t* xs, const void* g, const int64_t* gs,
+                   const void* out, int dtype, int64_t batch, int n, int64_t cols) {
+  if (n < 5 || n > 8 || !known_dtype(dtype) || batch < 0 || cols < 1)
     return fail(FH_ERR_INVALID_ARGUMENT,
-                "hc_mix: X and dY need contiguous, 16-byte aligned rows whose length C and strides are multiples of " +
-                    std::to_string(v) + " elements");
+                "hc_apply: expected E [B, n, n] (float32) and X [B, n, C] with 5 <= n <= 8, C >= 1, in float32, "
+                "float16, or bfloat16");
+  if (batch == 0) return FH_OK;
+  if (e == nullptr || x == nullptr || xs == nullptr || out == nullptr)
+    return fail(FH_ERR_INVALID_ARGUMENT, "hc_apply: null pointer");
+  if (!aligned(e, 4)) return fail(FH_ERR_INVALID_ARGUMENT, "hc_apply: E must be 4-byte aligned float32");
+  if (!stream_rows_ok(x, xs, n, cols, dtype) || (g != nullptr && !stream_rows_ok(g, gs, n, cols, dtype)) ||
+      !aligned(out, 16))
+    return fail(FH_ERR_INVALID_ARGUMENT, rows_message("hc_apply", dtype));
   return FH_OK;
 }
 
@@ -230,6 +255,32 @@ int fh_hc_mix_backward(const void* h, const int64_t h_strides[3], int h_neg, con
                                            grad_strides, dx, dh, de_out, dtype, batch, n, cols, stream);
   if (err != hipSuccess) return fail(FH_ERR_LAUNCH, std::string("kernel launch failed: ") + hipGetErrorString(err));
   g_error.clear();
+  return FH_OK;
+}
+
+int fh_hc_apply(const float* e, const void* x, const int64_t x_strides[3], void* y, int dtype, int64_t batch, int n,
+                int64_t cols, hipStream_t stream) {
+  g_error.clear();
+  const int rc = validate_apply(e, x, x_strides, nullptr, nullptr, y, dtype, batch, n, cols);
+  if (rc != FH_OK || batch == 0) return rc;
+  const hipError_t err =
+      fh::launch_hc_apply(e, x, x_strides, nullptr, nullptr, y, nullptr, dtype, batch, n, cols, stream);
+  if (err != hipSuccess) return fail(FH_ERR_LAUNCH, std::string("kernel launch failed: ") + hipGetErrorString(err));
+  return FH_OK;
+}
+
+int fh_hc_apply_backward(const float* e, const void* x, const int64_t x_strides[3], const void* grad,
+                         const int64_t grad_strides[3], void* dx, float* de, int dtype, int64_t batch, int n,
+                         int64_t cols, hipStream_t stream) {
+  g_error.clear();
+  const int rc = validate_apply(e, x, x_strides, grad, grad_strides, dx, dtype, batch, n, cols);
+  if (rc != FH_OK) return rc;
+  if (batch > 0 && (grad == nullptr || de == nullptr))
+    return fail(FH_ERR_INVALID_ARGUMENT, "hc_apply: null grad or de pointer");
+  if (batch > 0 && !aligned(de, 4)) return fail(FH_ERR_INVALID_ARGUMENT, "hc_apply: dE must be 4-byte aligned float32");
+  if (batch == 0) return FH_OK;
+  const hipError_t err = fh::launch_hc_apply(e, x, x_strides, grad, grad_strides, dx, de, dtype, batch, n, cols, stream);
+  if (err != hipSuccess) return fail(FH_ERR_LAUNCH, std::string("kernel launch failed: ") + hipGetErrorString(err));
   return FH_OK;
 }
 

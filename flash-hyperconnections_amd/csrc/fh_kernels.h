@@ -27,6 +27,10 @@ Operand hc_operand(const void* h, const int64_t strides[3], int neg, int dtype);
 hipError_t launch_hc_mix(const Operand& h, const void* x, const int64_t* xs, const void* gy, const int64_t* gs,
                          void* out, void* dh, float* aux, int dtype, int64_t batch, int n, int64_t cols,
                          hipStream_t stream);
+// exp(H) supplied in FP32 (5 <= n <= 8): gy == nullptr applies it (out = E X);
+// otherwise out = E^T dY and de = dY X^T (FP32).
+hipError_t launch_hc_apply(const float* e, const void* x, const int64_t* xs, const void* gy, const int64_t* gs,
+                           void* out, float* de, int dtype, int64_t batch, int n, int64_t cols, hipStream_t stream);
 // (degree, s) and FP64 norm per matrix.
 hipError_t launch_params(const ExpmArgs& args, int dtype, bool pair, int32_t* params, double* norms,
                          hipStream_t stream);

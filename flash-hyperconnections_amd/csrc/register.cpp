@@ -2,8 +2,9 @@
 // the reference's csrc/register.cpp and the ATen half of csrc/matrix_exp.cu).
 //
 // Schemas are the reference's (csrc/register.cpp:10-13) plus two debug ops and
-// the fused hyper-connection stream mixing (_hc_mix, its backward and a debug
-// variant), which has no counterpart in the reference.
+// the hyper-connection stream mixing (_hc_mix, its backward and a debug
+// variant, fused with exp(h) for 2 <= n <= 4; _hc_apply and its backward with
+// exp(h) supplied, for 5 <= n <= 8), which has no counterpart in the reference.
 // The implementations sit on the CUDA dispatch key, which ROCm tensors use.
 // Each one checks its inputs with the reference's messages
 // (csrc/matrix_exp.cu:52-59), allocates the contiguous output in the input
@@ -211,6 +212,63 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> hc_mix_aux_hip(const at::Tensor& 
   return r;
 }
 
+// ---- stream mixing with exp(h) supplied, 5 <= n <= 8 ------------------------
+
+void check_apply(const at::Tensor& e, const at::Tensor& x) {
+  TORCH_CHECK(e.is_cuda() && e.layout() == at::kStrided && e.dim() == 3 && e.size(-1) == e.size(-2) &&
+                  e.size(-1) >= 5 && e.size(-1) <= 8 && e.scalar_type() == at::kFloat,
+              "hc_apply: expected a strided CUDA float32 [B, n, n] tensor e, 5 <= n <= 8");
+  TORCH_CHECK(x.device() == e.device() && x.layout() == at::kStrided && x.dim() == 3 && x.size(0) == e.size(0) &&
+                  x.size(1) == e.size(1) && x.size(2) >= 1 &&
+                  (x.scalar_type() == at::kFloat || x.scalar_type() == at::kHalf ||
+                   x.scalar_type() == at::kBFloat16),
+              "hc_apply: expected x [B, n, C] on e's device, C >= 1, in float32, float16, or bfloat16");
+}
+
+// (y, empty) forward; (dx, dE) backward.
+std::tuple<at::Tensor, at::Tensor> apply_run(const at::Tensor& e, const at::Tensor& x,
+                                             const std::optional<at::Tensor>& grad) {
+  check_apply(e, x);
+  if (grad) TORCH_CHECK(grad->sizes() == x.sizes() && grad->device() == x.device() &&
+                            grad->scalar_type() == x.scalar_type(),
+                        "hc_apply: grad must match x");
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(e.device());
+  const int64_t B = e.size(0), n = e.size(1), C = x.size(2);
+  const at::Tensor ec = e.resolve_neg().contiguous();
+  const at::Tensor xs = streamable(x);
+  const int64_t Cp = xs.size(2);
+  at::Tensor out = at::empty({B, n, Cp}, x.options());
+  at::Tensor de = grad ? at::empty({B, n, n}, e.options()) : at::empty({0}, e.options());
+  if (B > 0) {
+    const int64_t x_strides[3] = {xs.stride(0), xs.stride(1), xs.stride(2)};
+    if (grad) {
+      at::Tensor gs = streamable(*grad);
+      if (gs.size(2) != Cp) {
+        at::Tensor p = at::zeros({B, n, Cp}, gs.options());
+        p.narrow(2, 0, C).copy_(gs.narrow(2, 0, C));
+        gs = p;
+      }
+      const int64_t g_strides[3] = {gs.stride(0), gs.stride(1), gs.stride(2)};
+      check_status(fh_hc_apply_backward(ec.const_data_ptr<float>(), xs.const_data_ptr(), x_strides,
+                                        gs.const_data_ptr(), g_strides, out.mutable_data_ptr(),
+                                        de.mutable_data_ptr<float>(), dtype_code(x.scalar_type()), B,
+                                        static_cast<int>(n), Cp, current_stream()));
+    } else {
+      check_status(fh_hc_apply(ec.const_data_ptr<float>(), xs.const_data_ptr(), x_strides, out.mutable_data_ptr(),
+                               dtype_code(x.scalar_type()), B, static_cast<int>(n), Cp, current_stream()));
+    }
+  }
+  if (Cp != C) out = out.narrow(2, 0, C).contiguous();
+  return {out, de};
+}
+
+at::Tensor hc_apply_hip(const at::Tensor& e, const at::Tensor& x) { return std::get<0>(apply_run(e, x, std::nullopt)); }
+
+std::tuple<at::Tensor, at::Tensor> hc_apply_backward_hip(const at::Tensor& e, const at::Tensor& x,
+                                                         const at::Tensor& grad) {
+  return apply_run(e, x, grad);
+}
+
 using MatrixExpOp = c10::TypedOperatorHandle<at::Tensor(const at::Tensor&)>;
 using FrechetOp = c10::TypedOperatorHandle<at::Tensor(const at::Tensor&, const at::Tensor&)>;
 
@@ -296,6 +354,8 @@ TORCH_LIBRARY(flash_hypercons, m) {
   m.def("_hc_mix(Tensor h, Tensor x) -> Tensor");
   m.def("_hc_mix_backward(Tensor h, Tensor x, Tensor grad) -> (Tensor, Tensor)");
   m.def("_hc_mix_aux(Tensor h, Tensor x, Tensor? grad) -> (Tensor, Tensor, Tensor)");
+  m.def("_hc_apply(Tensor e, Tensor x) -> Tensor");
+  m.def("_hc_apply_backward(Tensor e, Tensor x, Tensor grad) -> (Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(flash_hypercons, CUDA, m) {
@@ -306,6 +366,8 @@ TORCH_LIBRARY_IMPL(flash_hypercons, CUDA, m) {
   m.impl("_hc_mix", &flash_hypercons::hc_mix_hip);
   m.impl("_hc_mix_backward", &flash_hypercons::hc_mix_backward_hip);
   m.impl("_hc_mix_aux", &flash_hypercons::hc_mix_aux_hip);
+  m.impl("_hc_apply", &flash_hypercons::hc_apply_hip);
+  m.impl("_hc_apply_backward", &flash_hypercons::hc_apply_backward_hip);
 }
 
 TORCH_LIBRARY_IMPL(flash_hypercons, Autograd, m) { m.impl("_matrix_exp", &flash_hypercons::matrix_exp_autograd); }

@@ -4,13 +4,20 @@
 ``[B, n, n]`` (the per-token mixing generator) and ``x`` of shape ``[B, n, C]``
 (the n residual streams of each token).  The reference stops at
 ``matrix_exp(h)`` (ops/matrix_exp/__init__.py:80-97) and leaves the product to
-the caller; on a gfx950 device with 2 <= n <= 4 and float32 / float16 /
-bfloat16 operands of one dtype this build computes the product in the same
-kernel that computes exp(h), so exp(h) never goes through memory, and the
-backward is one kernel as well (dX = exp(h)^T dY, dE = dY X^T reduced on chip,
-dH = L(h^T, dE)).  Everything else -- other n, CPU tensors, function
-transforms, forward-mode tangents, a backward that builds a graph -- is the
-composition ``matrix_exp(h) @ x`` with this package's ``matrix_exp``.
+the caller; on a gfx950 device with float32 / float16 / bfloat16 operands of
+one dtype this build streams x once per direction:
+
+* 2 <= n <= 4: the product is computed in the same kernel that computes
+  exp(h), so exp(h) never goes through memory, and the backward is one kernel
+  as well (dX = exp(h)^T dY, dE = dY X^T reduced on chip, dH = L(h^T, dE));
+* 5 <= n <= 8: exp(h) is computed in FP32 by ``matrix_exp`` (a few bytes per
+  token next to x's n*C elements) and applied by a streaming kernel; the
+  backward is one streaming kernel for dX and dE followed by the Frechet
+  kernel for dH.
+
+Everything else -- other n, CPU tensors, function transforms, forward-mode
+tangents, a backward that builds a graph -- is the composition
+``matrix_exp(h) @ x`` with this package's ``matrix_exp``.
 """
 
 import torch
@@ -21,7 +28,8 @@ from flash_hypercons.ops.matrix_exp import _device_supported, _frechet_different
 _DTYPES = (torch.float32, torch.float16, torch.bfloat16)
 
 
-def _fused(h: torch.Tensor, x: torch.Tensor) -> bool:
+def _streamed(h: torch.Tensor, x: torch.Tensor) -> bool:
+    """Operands the streaming kernels take (any n; the callers pick the n range)."""
     return (
         isinstance(h, torch.Tensor)
         and isinstance(x, torch.Tensor)
@@ -36,7 +44,6 @@ def _fused(h: torch.Tensor, x: torch.Tensor) -> bool:
         and h.ndim == 3
         and x.ndim == 3
         and h.shape[-1] == h.shape[-2]
-        and 2 <= h.shape[-1] <= 4
         and x.shape[0] == h.shape[0]
         and x.shape[1] == h.shape[1]
         and x.shape[2] >= 1
@@ -67,6 +74,27 @@ def _hc_mix_aux_fake(h, x, grad):
     return x.new_empty(x.shape), second, h.new_empty(h.shape, dtype=torch.float32)
 
 
+def _fused(h: torch.Tensor, x: torch.Tensor) -> bool:
+    return _streamed(h, x) and 2 <= h.shape[-1] <= 4
+
+
+def _applied(h: torch.Tensor, x: torch.Tensor) -> bool:
+    return _streamed(h, x) and 5 <= h.shape[-1] <= 8
+
+
+@torch.library.register_fake("flash_hypercons::_hc_apply")
+def _hc_apply_fake(e, x):
+    torch._check(e.ndim == 3 and x.ndim == 3)
+    torch._check(x.shape[0] == e.shape[0] and x.shape[1] == e.shape[1])
+    return x.new_empty(x.shape)
+
+
+@torch.library.register_fake("flash_hypercons::_hc_apply_backward")
+def _hc_apply_backward_fake(e, x, grad):
+    torch._check(grad.shape == x.shape)
+    return x.new_empty(x.shape), e.new_empty(e.shape)
+
+
 class _MixStreams(torch.autograd.Function):
     @staticmethod
     def forward(h, x):
@@ -86,14 +114,42 @@ class _MixStreams(torch.autograd.Function):
         return dh, dx
 
 
+class _MixStreamsApplied(torch.autograd.Function):
+    """5 <= n <= 8: E = exp(h) in FP32 (the P = 8 kernel), then y = E x streamed;
+    backward: (dX, dE) in one streaming pass, dH = L(h^T, dE) in FP32, rounded to h's dtype."""
+
+    @staticmethod
+    def forward(h, x):
+        e = torch.ops.flash_hypercons._matrix_exp(h.float())
+        return torch.ops.flash_hypercons._hc_apply(e, x), e
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        ctx.save_for_backward(inputs[0], inputs[1], output[1])
+        ctx.mark_non_differentiable(output[1])
+
+    @staticmethod
+    def backward(ctx, grad, _grad_e):
+        h, x, e = ctx.saved_tensors
+        if torch.is_grad_enabled():
+            return _frechet_differentiable(h.mT, grad @ x.mT), matrix_exp(h).mT @ grad
+        dx, de = torch.ops.flash_hypercons._hc_apply_backward(e, x, grad.contiguous())
+        dh = torch.ops.flash_hypercons._frechet(h.float().mT, de).to(h.dtype)
+        return dh, dx
+
+
 def mix_streams(h: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
     """exp(h) @ x per token: h [B, n, n], x [B, n, C] -> [B, n, C] (hyper-connection stream mixing).
 
-    Differentiable in both arguments.  Fused into one HIP kernel per direction for
-    2 <= n <= 4 on gfx950; otherwise composed from ``matrix_exp`` and a batched product.
+    Differentiable in both arguments.  On gfx950: fused into one HIP kernel per
+    direction for 2 <= n <= 4; for 5 <= n <= 8, exp(h) from ``matrix_exp`` in FP32
+    and one streaming kernel per direction.  Otherwise composed from
+    ``matrix_exp`` and a batched product.
     """
     if _fused(h, x):
         return _MixStreams.apply(h, x)
+    if _applied(h, x):
+        return _MixStreamsApplied.apply(h, x)[0]
     return matrix_exp(h) @ x
 
 

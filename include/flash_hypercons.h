@@ -121,6 +121,24 @@ FH_API int fh_hc_mix_backward(const void* h, const int64_t h_strides[3], int h_n
                        const int64_t x_strides[3], const void* grad, const int64_t grad_strides[3], void* dh,
                        void* dx, float* de_out, int dtype, int64_t batch, int n, int64_t cols, hipStream_t stream);
 
+/* Stream mixing for 5 <= n <= 8 streams with exp(h) supplied: y[b] = e[b] x[b]
+ * for e FP32 [batch, n, n] (contiguous; e.g. fh_matrix_exp of h in float32,
+ * which gives the same bits the fused path keeps on chip) and x [batch, n,
+ * cols] under fh_hc_mix's row rules; y contiguous [batch, n, cols] in the
+ * dtype of x.  No counterpart in the reference (the consumer product of its
+ * matrix_exp, ops/matrix_exp/__init__.py:80-97).  Allocates nothing. */
+FH_API int fh_hc_apply(const float* e, const void* x, const int64_t x_strides[3], void* y, int dtype, int64_t batch,
+                int n, int64_t cols, hipStream_t stream);
+
+/* Gradients through fh_hc_apply for the upstream gradient grad (x's layout
+ * rules): dx = e^T grad (contiguous [batch, n, cols]) and de = grad x^T (FP32
+ * [batch, n, n], contiguous), reduced in a fixed order; dh then follows as the
+ * Frechet derivative L(h^T, de) (fh_frechet in float32).  One kernel;
+ * allocates nothing. */
+FH_API int fh_hc_apply_backward(const float* e, const void* x, const int64_t x_strides[3], const void* grad,
+                         const int64_t grad_strides[3], void* dx, float* de, int dtype, int64_t batch, int n,
+                         int64_t cols, hipStream_t stream);
+
 /* Message of the last failing call on this thread ("" if none). */
 FH_API const char* fh_last_error(void);
 

@@ -31,7 +31,7 @@ def load():
 def test_headers_declare_entry_points():
     names = declared_functions()
     assert {"fh_matrix_exp", "fh_frechet", "fh_expm_launch", "fh_expm_params", "fh_hc_mix", "fh_hc_mix_backward",
-            "fh_last_error", "fh_version"} <= set(names)
+            "fh_hc_apply", "fh_hc_apply_backward", "fh_last_error", "fh_version"} <= set(names)
 
 
 @pytest.mark.parametrize("name", declared_functions())
@@ -103,13 +103,50 @@ def test_hc_mix_validation_without_gpu():
     assert b"null grad or dh" in lib.fh_last_error()
 
 
+def test_hc_apply_validation_without_gpu():
+    lib = load()
+    lib.fh_last_error.restype = ctypes.c_char_p
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+    lib.fh_hc_apply.argtypes = [vp, vp, vp, vp, i32, i64, i32, i64, vp]
+    lib.fh_hc_apply_backward.argtypes = [vp, vp, vp, vp, vp, vp, vp, i32, i64, i32, i64, vp]
+    xs = (ctypes.c_int64 * 3)(8 * 64, 64, 1)
+    fake = 1 << 20  # never dereferenced: every call below returns before a HIP call
+    # n outside [5, 8], unknown dtype, C < 1.
+    for n, dtype, cols in ((4, 0, 64), (9, 0, 64), (6, 3, 64), (6, 0, 0)):
+        assert lib.fh_hc_apply(fake, fake, xs, fake, dtype, 2, n, cols, None) == 1
+        assert b"5 <= n <= 8" in lib.fh_last_error()
+    assert lib.fh_hc_apply(None, None, xs, None, 0, 0, 8, 64, None) == 0
+    assert lib.fh_hc_apply(None, fake, xs, fake, 0, 2, 8, 64, None) == 1
+    assert b"null pointer" in lib.fh_last_error()
+    assert lib.fh_hc_apply(fake + 2, fake, xs, fake, 0, 2, 8, 64, None) == 1
+    assert b"4-byte aligned" in lib.fh_last_error()
+    # Rows: the rule of fh_hc_mix (BF16: C and strides in multiples of 8 elements).
+    for strides, ptr, cols in (
+        ((ctypes.c_int64 * 3)(8 * 64, 64, 2), fake, 64),
+        ((ctypes.c_int64 * 3)(8 * 64, 68, 1), fake, 64),
+        (xs, fake, 60),
+        (xs, fake + 8, 64),
+        ((ctypes.c_int64 * 3)(0, 1 << 28, 1), fake, 64),  # one token spans more than 2 GiB
+    ):
+        assert lib.fh_hc_apply(fake, ptr, strides, fake, 1, 2, 8, cols, None) == 1
+        assert b"16-byte aligned rows" in lib.fh_last_error() and b"multiples of 8" in lib.fh_last_error()
+    bad = (ctypes.c_int64 * 3)(8 * 64, 64, 2)
+    assert lib.fh_hc_apply_backward(fake, fake, xs, fake, bad, fake, fake, 0, 2, 8, 64, None) == 1
+    assert b"16-byte aligned rows" in lib.fh_last_error()
+    assert lib.fh_hc_apply_backward(fake, fake, xs, None, xs, fake, fake, 0, 2, 8, 64, None) == 1
+    assert lib.fh_hc_apply_backward(fake, fake, xs, fake, xs, fake, None, 0, 2, 8, 64, None) == 1
+    assert b"null grad or de" in lib.fh_last_error()
+    assert lib.fh_hc_apply_backward(fake, fake, xs, fake, xs, fake, fake + 1, 0, 2, 8, 64, None) == 1
+    assert b"dE must be 4-byte aligned" in lib.fh_last_error()
+
+
 def test_extension_registers_operators():
     import torch
 
     import flash_hypercons  # noqa: F401
 
     for name in ("_matrix_exp", "_frechet", "_expm_params", "_expm_debug", "_hc_mix", "_hc_mix_backward",
-                 "_hc_mix_aux"):
+                 "_hc_mix_aux", "_hc_apply", "_hc_apply_backward"):
         assert hasattr(torch.ops.flash_hypercons, name)
     schema = str(torch.ops.flash_hypercons._matrix_exp.default._schema)
     assert schema == "flash_hypercons::_matrix_exp(Tensor input) -> Tensor"

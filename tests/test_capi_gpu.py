@@ -7,7 +7,9 @@ torch operator on the same logical operands (both run the same kernels), and,
 for n <= 8, with the CPU restatement; squaring counts from ``fh_expm_launch``
 and ``fh_expm_params`` with the restatement's; ``fh_hc_mix`` and
 ``fh_hc_mix_backward`` (exp(h) x and its gradients) with the mixing operators,
-and their exp(h) / dE side outputs with the restatement.  Operands: contiguous,
+and their exp(h) / dE side outputs with the restatement; ``fh_hc_apply`` and
+``fh_hc_apply_backward`` (5 <= n <= 8, exp(h) supplied) with the apply
+operators and their dE with the restatement's dh.  Operands: contiguous,
 transposed views, lazily negated storage and expanded (stride-0) batches.
 """
 
@@ -37,8 +39,10 @@ def _lib():
     lib.fh_expm_params.argtypes = [vp, vp, i32, vp, vp, i32, i32, i64, i32, vp, vp, vp]
     lib.fh_hc_mix.argtypes = [vp, vp, i32, vp, vp, vp, vp, i32, i64, i32, i64, vp]
     lib.fh_hc_mix_backward.argtypes = [vp, vp, i32, vp, vp, vp, vp, vp, vp, vp, i32, i64, i32, i64, vp]
+    lib.fh_hc_apply.argtypes = [vp, vp, vp, vp, i32, i64, i32, i64, vp]
+    lib.fh_hc_apply_backward.argtypes = [vp, vp, vp, vp, vp, vp, vp, i32, i64, i32, i64, vp]
     for f in (lib.fh_matrix_exp, lib.fh_frechet, lib.fh_expm_launch, lib.fh_expm_params, lib.fh_hc_mix,
-              lib.fh_hc_mix_backward):
+              lib.fh_hc_mix_backward, lib.fh_hc_apply, lib.fh_hc_apply_backward):
         f.restype = ctypes.c_int
     lib.fh_last_error.restype = ctypes.c_char_p
     return lib
@@ -220,3 +224,37 @@ def test_hc_mix_rejects_unstreamable_rows():
     rc = lib().fh_hc_mix_backward(h.data_ptr(), hs, 0, x8.data_ptr(), x8s, None, x8s, h.data_ptr(), x8.data_ptr(),
                                   None, 0, 2, 4, 8, _stream())
     assert rc == 1 and b"null grad" in lib().fh_last_error()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n", [5, 8])
+def test_hc_apply_entry_points(n, dtype):
+    import flash_hypercons  # noqa: F401
+
+    batch, cols = 21, 136
+    hv, _ = _values(batch, n, dtype, seed=41 + n + CODES[dtype])
+    ops = torch.ops.flash_hypercons
+    e = ops._matrix_exp(hv.float())
+    # x and dY as row views inside wider rows (token-major storage), streamed in place.
+    x = torch.randn(n, batch, cols + 24, device="cuda").to(dtype).transpose(0, 1)[..., :cols]
+    gy = torch.randn(batch, n, cols, device="cuda").to(dtype)
+    xs, gs = I64x3(*x.stride()), I64x3(*gy.stride())
+    y = torch.empty(batch, n, cols, dtype=dtype, device="cuda")
+    rc = lib().fh_hc_apply(e.data_ptr(), x.data_ptr(), xs, y.data_ptr(), CODES[dtype], batch, n, cols, _stream())
+    assert rc == 0, lib().fh_last_error()
+    dx = torch.empty_like(y)
+    de = torch.empty(batch, n, n, device="cuda")
+    rc = lib().fh_hc_apply_backward(e.data_ptr(), x.data_ptr(), xs, gy.data_ptr(), gs, dx.data_ptr(), de.data_ptr(),
+                                    CODES[dtype], batch, n, cols, _stream())
+    assert rc == 0, lib().fh_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(y, ops._hc_apply(e, x))
+    dx_op, de_op = ops._hc_apply_backward(e, x, gy)
+    assert torch.equal(dx, dx_op) and torch.equal(de, de_op)
+    exp_e, _, _ = oracle.matrix_exp_f32(oracle.tensor_to_f32(hv))
+    assert torch.equal(e.cpu(), torch.from_numpy(exp_e))
+    # The public op's dh is the restatement's L(h^T, dE) on this dE, rounded to the dtype.
+    hr = hv.clone().requires_grad_()
+    flash_hypercons.mix_streams(hr, x).backward(gy)
+    exp_dh, _, _ = oracle.matrix_exp_f32(oracle.tensor_to_f32(hv.mT), de.cpu().numpy())
+    assert torch.equal(hr.grad.cpu(), oracle.round_to_dtype(exp_dh, dtype))

@@ -20,8 +20,9 @@ direction for 2 <= n <= 4.  Checks, on the GPU:
   non-unit column stride, C not a multiple of the 16-byte vector) give the same
   bits as contiguous operands; results do not depend on the batch around a
   token; non-finite h gives NaN for that token only;
-* everything the fusion does not cover (n = 5, CPU, forward-mode tangents,
-  function transforms) is the composed ``matrix_exp(h) @ x``.
+* everything the streaming kernels do not cover (n = 9, CPU, forward-mode
+  tangents, function transforms) is the composed ``matrix_exp(h) @ x``
+  (5 <= n <= 8 has its own kernels, tested in tests/test_hc_apply.py).
 """
 
 import pytest
@@ -264,7 +265,7 @@ def test_nonfinite_x_stays_in_its_column():
 
 @pytest.mark.gpu
 def test_outside_the_fusion_is_the_composition():
-    h, x = _inputs(5, 5, 40, torch.float32)
+    h, x = _inputs(5, 9, 40, torch.float32)
     assert same_bits(fh.mix_streams(h, x), fh.matrix_exp(h) @ x)
     h4, x4 = _inputs(5, 4, 40, torch.float32)
     # Forward-mode tangents and function transforms take the composed path.

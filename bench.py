@@ -267,17 +267,38 @@ def make_mix_inputs(torch, device, shape=MIX_SHAPE, dtype=None):
     return h, x, g
 
 
-def measure_mix(torch, fh, steps: int, warmup: int, trials: int, device, keep: bool) -> tuple[dict, dict]:
-    """``fh.mix_streams`` (y = exp(h) x fused, one kernel per direction) against the composed
-    ``fh.matrix_exp(h) @ x`` (exp kernel, then torch's batched product) on the same inputs: the
-    forward alone, and forward + autograd backward of both operands.  HBM roofline of each fused
-    kernel from its algorithmic bytes: forward reads h and x and writes y; backward reads h, x and
-    dy and writes dh and dx."""
-    h, x, g = make_mix_inputs(torch, device)
+MIX_WIDE_SHAPE = (16384, 8, 4096)  # the 8-stream case: exp(h) from the P = 8 kernel, then apply
+
+
+def measure_mix(torch, fh, steps: int, warmup: int, trials: int, device, keep: bool,
+                shape=MIX_SHAPE) -> tuple[dict, dict]:
+    """``fh.mix_streams`` against the composed ``fh.matrix_exp(h) @ x`` (exp kernel, then torch's
+    batched product) on the same inputs: the forward alone, and forward + autograd backward of
+    both operands.  n <= 4: y = exp(h) x fused, one kernel per direction; HBM roofline of each
+    from its algorithmic bytes (forward reads h and x and writes y; backward reads h, x and dy and
+    writes dh and dx).  5 <= n <= 8: the streaming apply kernels (forward reads E in FP32 and x,
+    writes y; backward reads E, x and dy, writes dx and dE in FP32), with the exponential and
+    Frechet launches of the step on top."""
+    h, x, g = make_mix_inputs(torch, device, shape=shape)
     tokens, n, cols = x.shape
     es = x.element_size()
     ops = torch.ops.flash_hypercons
     hr, xr = h.clone().requires_grad_(), x.clone().requires_grad_()
+    wide = n > 4
+    if wide:
+        e = ops._matrix_exp(h.float())
+        fwd_kernel, bwd_kernel = (lambda: ops._hc_apply(e, x)), (lambda: ops._hc_apply_backward(e, x, g))
+        bytes_fwd = tokens * (4 * n * n + 2 * n * cols * es)
+        bytes_bwd = tokens * (8 * n * n + 3 * n * cols * es)
+        short = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}[x.dtype]
+        key = f"hc_apply_{{}}_{short}_n{n}"
+        summary = "hc_apply_hbm_traffic.md"
+    else:
+        fwd_kernel, bwd_kernel = (lambda: ops._hc_mix(h, x)), (lambda: ops._hc_mix_backward(h, x, g))
+        bytes_fwd = tokens * (n * n + 2 * n * cols) * es
+        bytes_bwd = tokens * (2 * n * n + 3 * n * cols) * es
+        key = "hc_mix_{}_bf16_n4"
+        summary = "hc_mix_hbm_traffic.md"
 
     def fused_step():
         return torch.autograd.grad(fh.mix_streams(hr, xr), (hr, xr), g)
@@ -285,16 +306,15 @@ def measure_mix(torch, fh, steps: int, warmup: int, trials: int, device, keep: b
     def composed_step():
         return torch.autograd.grad(fh.matrix_exp(hr) @ xr, (hr, xr), g)
 
-    t_fwd = time_trials(torch, lambda: ops._hc_mix(h, x), kernel_launches(steps, trials), warmup, trials)
-    t_bwd = time_trials(torch, lambda: ops._hc_mix_backward(h, x, g), kernel_launches(steps, trials), warmup, trials)
+    t_fwd = time_trials(torch, fwd_kernel, kernel_launches(steps, trials), warmup, trials)
+    t_bwd = time_trials(torch, bwd_kernel, kernel_launches(steps, trials), warmup, trials)
     t_step = time_trials(torch, fused_step, steps, warmup, trials)
     t_cfwd = time_trials(torch, lambda: fh.matrix_exp(h) @ x, steps, warmup, trials)
     t_cstep = time_trials(torch, composed_step, steps, warmup, trials)
-    bytes_fwd = tokens * (n * n + 2 * n * cols) * es
-    bytes_bwd = tokens * (2 * n * n + 3 * n * cols) * es
     ms_f, ms_b = t_fwd["median_ms"], t_bwd["median_ms"]
     out = {
         "workload": "fh.mix_streams: y = exp(h) @ x per token, h [T, n, n], x [T, n, C]",
+        "path": "exp (P = 8 kernel) + streaming apply" if wide else "fused",
         "shape": [tokens, n, cols],
         "dtype": str(x.dtype).replace("torch.", ""),
         "tokens_per_s_fwd_bwd": tokens / (t_step["median_ms"] * 1e-3),
@@ -311,14 +331,19 @@ def measure_mix(torch, fh, steps: int, warmup: int, trials: int, device, keep: b
         "speedup_step_vs_composed": t_cstep["median_ms"] / t_step["median_ms"],
         "fwd_kernel": {"bound": "hbm", "algorithmic_bytes": bytes_fwd, "achieved_gbs": bytes_fwd / (ms_f * 1e-3) / 1e9,
                        "frac": bytes_fwd / (ms_f * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                       "traffic": profiled_traffic("hc_mix_fwd_bf16_n4", "hc_mix_hbm_traffic.md")},
+                       "traffic": profiled_traffic(key.format("fwd"), summary)},
         "bwd_kernel": {"bound": "hbm", "algorithmic_bytes": bytes_bwd, "achieved_gbs": bytes_bwd / (ms_b * 1e-3) / 1e9,
                        "frac": bytes_bwd / (ms_b * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                       "traffic": profiled_traffic("hc_mix_bwd_bf16_n4", "hc_mix_hbm_traffic.md")},
+                       "traffic": profiled_traffic(key.format("bwd"), summary)},
         "roofline_frac_step": (bytes_fwd + bytes_bwd) / (HBM_PEAK_GBS * 1e9) / (t_step["median_ms"] * 1e-3),
     }
     kept = {}
-    if keep:
+    if keep and wide:
+        y = fh.mix_streams(h, x)
+        dx, de = ops._hc_apply_backward(e, x, g)
+        dh = torch.autograd.grad(fh.mix_streams(hr, xr), hr, g)[0]
+        kept = {"h": h, "x": x, "g": g, "y": y, "e": e, "dx": dx, "dh": dh, "de": de}
+    elif keep:
         y, _, e = ops._hc_mix_aux(h, x, None)
         dx, dh, de = ops._hc_mix_aux(h, x, g)
         kept = {"h": h, "x": x, "g": g, "y": y, "e": e, "dx": dx, "dh": dh, "de": de}
@@ -493,19 +518,20 @@ def cpu_leg(torch, kept: dict, mix_kept: dict | None = None) -> dict:
         log(f"[bench] parity {name} ({time.perf_counter() - t0:.1f} s): {json.dumps(parity[name])}")
     failures = {f"{name}.{d}": why for name, rep in parity.items() for d, r in rep.items()
                 if (why := check(r, kept[name]["x"].shape[-1]))}
-    if mix_kept:
+    for name, k in (mix_kept or {}).items():
+        if not k:
+            continue
         from tests.mixcheck import check_mix, mix_parity
 
         t0 = time.perf_counter()
-        k = mix_kept
-        parity["hc"] = mix_parity(k["h"], k["x"], k["g"], k["y"], k["e"], k["dx"], k["dh"], k["de"], threads=threads)
-        log(f"[bench] parity hc ({time.perf_counter() - t0:.1f} s): {json.dumps(parity['hc'])}")
-        if why := check_mix(parity["hc"]):
-            failures["hc"] = why
+        parity[name] = mix_parity(k["h"], k["x"], k["g"], k["y"], k["e"], k["dx"], k["dh"], k["de"], threads=threads)
+        log(f"[bench] parity {name} ({time.perf_counter() - t0:.1f} s): {json.dumps(parity[name])}")
+        if why := check_mix(parity[name]):
+            failures[name] = why
     result["parity"] = {"pass": not failures, "failures": failures, "configs": parity,
                         "rule": "tests/fullsize.py check(): s == oracle for every matrix; n <= 8 bit-identical "
                         "to the oracle; strict north-star failures <= the oracle's; FP32 mean error <= 1.05x "
-                        "the oracle's; per-matrix excess over the oracle's error under a sanity cap. hc "
+                        "the oracle's; per-matrix excess over the oracle's error under a sanity cap. hc, hc8 "
                         "(tests/mixcheck.py): exp(h) and dh bit-identical to the oracle, y / dx / dE within "
                         "the FP32 summation bound of the FP64 products, every token"}
     return result
@@ -621,7 +647,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--trials", type=int, default=5, help="the K timed steps are split into this many trials")
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU leg (CPU baselines and parity)")
-    ap.add_argument("--only", default=None, help="comma list of configs (c2,c3,c4,c5,c5f32,p8,c2s8,hc)")
+    ap.add_argument("--only", default=None, help="comma list of configs (c2,c3,c4,c5,c5f32,p8,c2s8,hc,hc8)")
     ap.add_argument("--extras", action="store_true",
                     help="with --only: also run the reference table and the small-batch latency")
     ap.add_argument("--sweep", action="store_true",
@@ -651,13 +677,14 @@ def main() -> int:
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    configs = (args.only or "c2,c3,c4,c5,c5f32,p8,c2s8,hc").split(",")
-    results, kept, mix_kept = {}, {}, None
+    configs = (args.only or "c2,c3,c4,c5,c5f32,p8,c2s8,hc,hc8").split(",")
+    results, kept, mix_kept = {}, {}, {}
     for name in configs:
         log(f"[bench] {name} ...")
-        if name == "hc":
-            results[name], mix_kept = measure_mix(torch, fh, args.steps, args.warmup, args.trials, device,
-                                                  keep=not args.skip_cpu)
+        if name in ("hc", "hc8"):
+            results[name], mix_kept[name] = measure_mix(torch, fh, args.steps, args.warmup, args.trials, device,
+                                                        keep=not args.skip_cpu,
+                                                        shape=MIX_SHAPE if name == "hc" else MIX_WIDE_SHAPE)
             log(f"[bench] {name}: {json.dumps(results[name])}")
             continue
         results[name], k = measure_config(name, torch, fh, args.steps, args.warmup, args.trials, device,

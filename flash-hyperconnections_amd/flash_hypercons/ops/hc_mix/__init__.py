@@ -119,22 +119,19 @@ class _MixStreamsApplied(torch.autograd.Function):
     backward: (dX, dE) in one streaming pass, dH = L(h^T, dE) in FP32, rounded to h's dtype."""
 
     @staticmethod
-    def forward(h, x):
-        e = torch.ops.flash_hypercons._matrix_exp(h.float())
-        return torch.ops.flash_hypercons._hc_apply(e, x), e
+    def forward(ctx, h, x):
+        hf = h.float()
+        e = torch.ops.flash_hypercons._matrix_exp(hf)
+        ctx.save_for_backward(h, x, e, hf)
+        return torch.ops.flash_hypercons._hc_apply(e, x)
 
     @staticmethod
-    def setup_context(ctx, inputs, output):
-        ctx.save_for_backward(inputs[0], inputs[1], output[1])
-        ctx.mark_non_differentiable(output[1])
-
-    @staticmethod
-    def backward(ctx, grad, _grad_e):
-        h, x, e = ctx.saved_tensors
+    def backward(ctx, grad):
+        h, x, e, hf = ctx.saved_tensors
         if torch.is_grad_enabled():
             return _frechet_differentiable(h.mT, grad @ x.mT), matrix_exp(h).mT @ grad
         dx, de = torch.ops.flash_hypercons._hc_apply_backward(e, x, grad.contiguous())
-        dh = torch.ops.flash_hypercons._frechet(h.float().mT, de).to(h.dtype)
+        dh = torch.ops.flash_hypercons._frechet(hf.mT, de).to(h.dtype) if ctx.needs_input_grad[0] else None
         return dh, dx
 
 
@@ -149,7 +146,7 @@ def mix_streams(h: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
     if _fused(h, x):
         return _MixStreams.apply(h, x)
     if _applied(h, x):
-        return _MixStreamsApplied.apply(h, x)[0]
+        return _MixStreamsApplied.apply(h, x)
     return matrix_exp(h) @ x
 
 

@@ -132,6 +132,34 @@ def test_graph_building_backward():
     assert err.max().item() < 1e-4, err
 
 
+@pytest.mark.gpu
+def test_gradient_of_one_operand():
+    h, x = _inputs(9, 6, 72, torch.bfloat16)
+    g = torch.randn_like(x, dtype=torch.float32).to(torch.bfloat16)
+    xr = x.clone().requires_grad_()
+    fh.mix_streams(h, xr).backward(g)
+    hr = h.clone().requires_grad_()
+    fh.mix_streams(hr, x).backward(g)
+    dx, de = OPS._hc_apply_backward(_exp(h), x, g)
+    assert same_bits(xr.grad, dx)
+    assert same_bits(hr.grad, OPS._frechet(h.float().mT, de).to(torch.bfloat16))
+
+
+@pytest.mark.gpu
+@pytest.mark.compile
+def test_compile_keeps_the_apply_operators():
+    h, x = _inputs(16, 8, 128, torch.bfloat16)
+    g = torch.randn_like(x, dtype=torch.float32).to(torch.bfloat16)
+    compiled = torch.compile(lambda a, b: fh.mix_streams(a, b), fullgraph=True)
+    hr, xr = h.clone().requires_grad_(), x.clone().requires_grad_()
+    y = compiled(hr, xr)
+    y.backward(g)
+    assert same_bits(y, fh.mix_streams(h, x))
+    he, xe = h.clone().requires_grad_(), x.clone().requires_grad_()
+    fh.mix_streams(he, xe).backward(g)
+    assert same_bits(hr.grad, he.grad) and same_bits(xr.grad, xe.grad)
+
+
 def _x_view(x, layout):
     b, n, c = x.shape
     if layout == "contiguous":

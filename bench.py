@@ -6,7 +6,9 @@ upstream gradient N(0, 1); one step = ``fh.matrix_exp`` forward plus
 Metric: matrices per second of forward + backward.  The K timed steps are split
 into >= 5 trials, each bracketed by a device synchronisation and timed with HIP
 events on the stream the kernels run on; ``ms_per_step`` is the median over the
-trials of the per-step time (every trial's time is kept in ``trials_ms``).
+trials of the per-step time (every trial's time is kept in ``trials_ms``).  Before
+its W warmup steps each config runs its step untimed for ``--settle`` seconds
+(default 0.3 s), so that the device has left its idle clocks when timing starts.
 
 Also reported in the same JSON line:
 * ``roofline`` -- the dominant kernel of that step (the P = 4 Frechet kernel):
@@ -36,7 +38,7 @@ Also reported in the same JSON line:
   figures; ``stock_gpu`` -- native torch.linalg.matrix_exp + autograd on this
   GPU in the same sweep; ``small_batch_latency`` -- B = 1 wall time per call.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--trials T] [--skip-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--trials T] [--settle S] [--skip-cpu]
                        [--only c2,...] [--extras] [--sweep]
 """
 
@@ -150,6 +152,25 @@ def time_trials(torch, fn, steps: int, warmup: int, trials: int) -> dict:
             "mean_ms": sum(p * s for p, s in zip(per_call, split_trials(steps, trials))) / steps}
 
 
+def settle(torch, fn, seconds: float) -> int:
+    """Run fn back to back for about `seconds` of wall time, untimed, then synchronise: brings
+    the device from idle to the clocks it holds under sustained load before anything is timed
+    (measured: the first ~0.1 s of a config's steps ran 5-25% slower than the rest).  Returns the
+    number of calls."""
+    if seconds <= 0:
+        return 0
+    calls, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            fn()
+        calls += 8
+        torch.cuda.synchronize()
+    return calls
+
+
+SETTLE_S = 0.3  # set from --settle in main()
+
+
 def kernel_launches(steps: int, trials: int) -> int:
     """Launches of a single-kernel loop: at least 25 per trial, so that the queue runs ahead of the
     host and a trial's time is the kernels' own (its first launch's latency amortised)."""
@@ -175,6 +196,7 @@ def measure_config(name: str, torch, fh, steps: int, warmup: int, trials: int, d
     fwd = torch.ops.flash_hypercons._matrix_exp
     bwd = torch.ops.flash_hypercons._frechet
     xt = x.detach().mT
+    settle(torch, step, SETTLE_S)
     t_step = time_trials(torch, step, steps, warmup, trials)
     t_fwd = time_trials(torch, lambda: fwd(x), kernel_launches(steps, trials), warmup, trials)
     t_bwd = time_trials(torch, lambda: bwd(xt, g), kernel_launches(steps, trials), warmup, trials)
@@ -306,6 +328,7 @@ def measure_mix(torch, fh, steps: int, warmup: int, trials: int, device, keep: b
     def composed_step():
         return torch.autograd.grad(fh.matrix_exp(hr) @ xr, (hr, xr), g)
 
+    settle(torch, fused_step, SETTLE_S)
     t_fwd = time_trials(torch, fwd_kernel, kernel_launches(steps, trials), warmup, trials)
     t_bwd = time_trials(torch, bwd_kernel, kernel_launches(steps, trials), warmup, trials)
     t_step = time_trials(torch, fused_step, steps, warmup, trials)
@@ -641,11 +664,14 @@ def reference_table(torch, fh, device, sizes=(4, 8, 16, 32), batches=(65536,), d
 
 
 def main() -> int:
+    global SETTLE_S
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--trials", type=int, default=5, help="the K timed steps are split into this many trials")
+    ap.add_argument("--settle", type=float, default=SETTLE_S,
+                    help="seconds of untimed steps per config before its W warmup steps (device clocks settle)")
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU leg (CPU baselines and parity)")
     ap.add_argument("--only", default=None, help="comma list of configs (c2,c3,c4,c5,c5f32,p8,c2s8,hc,hc8)")
     ap.add_argument("--extras", action="store_true",
@@ -656,6 +682,7 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one device copy of exactly 64 MiB (profiler counter calibration)")
     args = ap.parse_args()
+    SETTLE_S = args.settle
     if args.gpus != 1:
         print(
             f"bench.py measures one GPU: the operator has no cross-GPU step (every matrix is independent; "
@@ -725,6 +752,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_s": args.settle,
         "ms_per_step": head["ms_step"] if head else None,
         "higher_is_better": True,
         "scaling": "weak",

@@ -38,6 +38,7 @@ KERNEL_SOURCES = [
     "expm_generic.hip",
     "expm_p4.hip",
     "expm_oct.hip",
+    "expm_oct16.hip",
     "expm_tile.hip",
     "expm_params.hip",
     "hc_mix.hip",

@@ -13,8 +13,10 @@ int64_t resident_blocks(const void* kernel, int block);
 hipError_t launch_generic(const ExpmArgs& args, int dtype, int P, bool pair, hipStream_t stream);
 // P == 4: one matrix per lane, 64 per wavefront, plain FP32 FMAs.
 hipError_t launch_p4(const ExpmArgs& args, int dtype, bool pair, hipStream_t stream);
-// P == 8: 4 matrices per wavefront as 2x2 blocks of 4x4x1 MFMA tiles.
+// P == 8: 4x4x1 MFMA blocks; the forward with 16 matrices per wavefront
+// (launch_oct16), the Frechet derivative with 4.
 hipError_t launch_oct(const ExpmArgs& args, int dtype, bool pair, hipStream_t stream);
+hipError_t launch_oct16(const ExpmArgs& args, int dtype, hipStream_t stream);
 // P in {16, 32}: one wavefront per matrix on 16x16x4 / 32x32x2 MFMA.
 hipError_t launch_tile(const ExpmArgs& args, int dtype, int P, bool pair, hipStream_t stream);
 // Fused hyper-connection stream mixing (n = 2..4): gy == nullptr selects the

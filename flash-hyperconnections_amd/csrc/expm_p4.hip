@@ -419,6 +419,171 @@ __global__ __launch_bounds__(64 * kP4Waves) __attribute__((amdgpu_waves_per_eu(P
   if (group == full && static_cast<int64_t>(full) * 64 < args.batch) expm_group_elements<T, Pair>(args, group, lane);
 }
 
+// ---- 2-byte dtypes: pairs of groups ordered by squaring count ---------------
+//
+// A wavefront squares up to the largest count among its 64 matrices, so when
+// counts spread (inputs over several decades of norm) most of a group's
+// squaring rounds run for a few lanes.  For FP16/BF16 a wavefront's LDS holds
+// two groups' inputs per slot, still double-buffered: the kernel computes the
+// count of all 128 matrices, ranks them by (count, position) with a counting
+// sort over ballots, and runs two rounds of 64 in rank order, so the first
+// round squares only up to the median count.  Each matrix's result (already in
+// the output dtype, 32 bytes) replaces its own first input tuples in the slot,
+// from where both groups are stored coalesced.  Which lane computes a matrix
+// does not change what it computes, so results are the unsorted kernel's.
+
+template <typename T, bool Pair>
+struct SortSlot {
+  static_assert(sizeof(typename T::storage) == 2, "pairs of groups fit the LDS budget for 2-byte dtypes only");
+  static constexpr int C = Raw<T>::C;                    // tuples per matrix (2)
+  static constexpr int kArea = C * kDenseRowBytes;       // one operand of one group
+  static constexpr int kGroup = (Pair ? 2 : 1) * kArea;  // one group's inputs
+  static constexpr int kBytes = 2 * kGroup;              // the batch's two groups
+};
+
+// Matrix m's tuples in an operand area of the slot (rows c * 1040, byte 16 m).
+template <typename T>
+__device__ __forceinline__ Raw<T> read_tuples_at(const char* area, int m) {
+  Raw<T> r;
+#pragma unroll
+  for (int c = 0; c < Raw<T>::C; ++c) r.q[c] = *reinterpret_cast<const uint4*>(area + c * kDenseRowBytes + 16 * m);
+  return r;
+}
+
+// A row-major result in the 2-byte output dtype, written over matrix m's input
+// tuples: tuple c holds output elements 8c .. 8c + 7.
+template <typename T>
+__device__ __forceinline__ void write_result_at(char* area, int m, const M4& v) {
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int e = 8 * c + 2 * k;
+      w[k] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(v.v[e]))) |
+             (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(v.v[e + 1]))) << 16);
+    }
+    *reinterpret_cast<uint4*>(area + c * kDenseRowBytes + 16 * m) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// Lanes below this one whose bit is set in `mask`.
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+  return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u)));
+}
+
+// Persistent kernel over batches of two full groups of a 2-byte dense batch
+// (n == 4): batch q is groups 2q and 2q + 1.
+template <typename T, bool Pair, int XL, int GL>
+__global__ __launch_bounds__(64 * kP4Waves) __attribute__((amdgpu_waves_per_eu(Pair ? 2 : 4, 8))) void expm_p4_sort_kernel(
+    ExpmArgs args) {
+  using Slot = SortSlot<T, Pair>;
+  constexpr int C = Slot::C;
+  constexpr int es = 2;
+  constexpr int kLoads = 2 * C * (Pair ? 2 : 1);  // load instructions per batch
+  constexpr int32_t kGroupBytes = 64 * 16 * es;
+  __shared__ __attribute__((aligned(16))) char tile_mem[kP4Waves][2][Slot::kBytes];
+  __shared__ uint8_t order_mem[kP4Waves][128];  // matrix (64 h + m) by rank
+  __shared__ int16_t count_mem[kP4Waves][128];  // squaring count by matrix
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // Groups fit in 32 bits: the host takes this kernel only for operands below 2 GiB.
+  const int32_t full = static_cast<int32_t>(args.batch / 64);
+  const int32_t batches = full / 2;
+  const int32_t stride = static_cast<int32_t>(gridDim.x) * kP4Waves;
+  int32_t q = static_cast<int32_t>(blockIdx.x) * kP4Waves + wave;
+  const U32x4 xs = rsrc_words(args.x.data);
+  const U32x4 gs = rsrc_words(Pair ? args.g.data : args.x.data);
+  const __amdgpu_buffer_rsrc_t out_rs = make_rsrc(args.out, 0x7FFFFFFFu);
+  uint8_t* order = order_mem[wave];
+  int16_t* count = count_mem[wave];
+  auto issue = [&](int32_t b, char* slot) {
+    const uint32_t a = lds_address(slot);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      load_group_to_lds<T>(xs, a + h * Slot::kGroup, (2 * b + h) * kGroupBytes, lane);
+      if constexpr (Pair) load_group_to_lds<T>(gs, a + h * Slot::kGroup + Slot::kArea, (2 * b + h) * kGroupBytes, lane);
+    }
+  };
+  auto matrix_at = [&](const char* grp, int m) {
+    PM<Pair> cur;
+    cur.d = decode<T, XL>(read_tuples_at<T>(grp, m));
+    if constexpr (Pair) cur.u = decode<T, GL>(read_tuples_at<T>(grp + Slot::kArea, m));
+    return cur;
+  };
+  int which = 0;
+  if (q < batches) issue(q, tile_mem[wave][0]);
+  for (; q < batches; q += stride) {
+    char* slot = tile_mem[wave][which];
+    if (q + stride < batches) {
+      issue(q + stride, tile_mem[wave][which ^ 1]);
+      wait_vm<kLoads>();
+    } else {
+      wait_vm<0>();
+    }
+    lds_order();
+    // Squaring count of matrix `lane` of each group (-1: non-finite, squares as 0).
+    int sh[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) sh[h] = lane_squarings<Pair>(matrix_at(slot + h * Slot::kGroup, lane));
+    // Rank by (count, matrix): counting sort, one ballot per count value and group.
+    const int k0 = sh[0] < 0 ? 0 : sh[0];
+    const int k1 = sh[1] < 0 ? 0 : sh[1];
+    int r0 = 0, r1 = 0, base = 0;
+    for (int v = 0; base < 128; ++v) {
+      const uint64_t b0 = __builtin_amdgcn_ballot_w64(k0 == v);
+      const uint64_t b1 = __builtin_amdgcn_ballot_w64(k1 == v);
+      if (k0 == v) r0 = base + lanes_below(b0);
+      base += __builtin_popcountll(b0);
+      if (k1 == v) r1 = base + lanes_below(b1);
+      base += __builtin_popcountll(b1);
+    }
+    order[r0] = static_cast<uint8_t>(lane);
+    order[r1] = static_cast<uint8_t>(64 + lane);
+    count[lane] = static_cast<int16_t>(sh[0]);  // at most ~130 for finite 2-byte inputs
+    count[64 + lane] = static_cast<int16_t>(sh[1]);
+    if (args.s_out) {
+      args.s_out[static_cast<int64_t>(2 * q) * 64 + lane] = sh[0];
+      args.s_out[static_cast<int64_t>(2 * q + 1) * 64 + lane] = sh[1];
+    }
+    lds_order();
+#pragma unroll 1
+    for (int r = 0; r < 2; ++r) {
+      const int id = order[64 * r + lane];
+      const int s = count[id];
+      char* grp = slot + (id >> 6) * Slot::kGroup;
+      const int m = id & 63;
+      const PM<Pair> a = scaled<Pair>(matrix_at(grp, m), s, args.x.sign, args.g.sign);
+      squarings<Pair>(t18<Pair>(a), s, [&](const M4& out) { write_result_at<T>(grp, m, out); });
+      if (s < 0) {  // rare: overwrite the result with NaN
+        M4 nan;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) nan.v[e] = __builtin_nanf("");
+        write_result_at<T>(grp, m, nan);
+      }
+    }
+    lds_order();
+    // Store instruction c of a group: lane l's tuple c, to tuple C l + c of the group's block.
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const uint4 v = *reinterpret_cast<const uint4*>(slot + h * Slot::kGroup + c * kDenseRowBytes + 16 * lane);
+        const U32x4 w = {v.x, v.y, v.z, v.w};
+        __builtin_amdgcn_raw_buffer_store_b128(w, out_rs, 16 * (C * lane + c), (2 * q + h) * kGroupBytes, 0);
+      }
+    lds_order();
+    which ^= 1;
+  }
+  // The odd last full group and the partial last group, if any, belong to the
+  // wavefront whose walk reaches the end of the batches.
+  if (q == batches) {
+    if (full % 2) expm_group_elements<T, Pair>(args, full - 1, lane);
+    if (static_cast<int64_t>(full) * 64 < args.batch) expm_group_elements<T, Pair>(args, full, lane);
+  }
+}
+
 // Every group of an element-class batch (n < 4 or strides no vector class
 // fits): per-element loads and stores.
 template <typename T, bool Pair>
@@ -460,10 +625,25 @@ hipError_t launch_dma(const ExpmArgs& args, hipStream_t stream) {
 }
 
 template <typename T, bool Pair, int XL, int GL>
+hipError_t launch_sort(const ExpmArgs& args, hipStream_t stream) {
+  static const int64_t resident =
+      resident_blocks(reinterpret_cast<const void*>(&expm_p4_sort_kernel<T, Pair, XL, GL>), 64 * kP4Waves);
+  // Batches of two full groups, plus the wavefront after them for the leftovers.
+  const int64_t units = args.batch / 128 + 1;
+  return launch_persistent(expm_p4_sort_kernel<T, Pair, XL, GL>, units, args, stream, resident);
+}
+
+template <typename T, bool Pair, int XL, int GL>
 hipError_t launch_vec_dense(const ExpmArgs& args, hipStream_t stream) {
   const bool xd = args.x.dense != 0;
   const bool gd = Pair && args.g.dense != 0;
-  if (xd && (!Pair || gd)) return launch_dma<T, Pair, XL, GL>(args, stream);
+  if (xd && (!Pair || gd)) {
+    if constexpr (sizeof(typename T::storage) == 2) {
+      return launch_sort<T, Pair, XL, GL>(args, stream);
+    } else {
+      return launch_dma<T, Pair, XL, GL>(args, stream);
+    }
+  }
   if (xd) {
     if constexpr (Pair) {
       return gd ? launch_vec<T, Pair, XL, GL, true, true>(args, stream)

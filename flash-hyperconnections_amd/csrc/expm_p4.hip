@@ -451,21 +451,51 @@ __device__ __forceinline__ Raw<T> read_tuples_at(const char* area, int m) {
 }
 
 // A row-major result in the 2-byte output dtype, written over matrix m's input
-// tuples: tuple c holds output elements 8c .. 8c + 7.
+// tuples: tuple c holds output elements 8c .. 8c + 7.  BF16 goes through
+// gfx950's packed conversion (round to nearest even, bit-identical to the
+// software rounding for every non-NaN value) unless a lane of the wavefront
+// holds a NaN, which the software rounding writes as the reference's 0x7FC0
+// whatever its sign and payload.  `nan_free`: the caller knows no lane can.
+typedef __bf16 BF16x2 __attribute__((ext_vector_type(2)));
+typedef float F32x2 __attribute__((ext_vector_type(2)));
+
 template <typename T>
-__device__ __forceinline__ void write_result_at(char* area, int m, const M4& v) {
+__device__ __forceinline__ void write_result_at(char* area, int m, const M4& v, bool nan_free) {
+  bool packed = false;
+  if constexpr (__is_same(T, BF16)) {
+    packed = nan_free;
+    if (!packed) {
+      float t = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) t += __builtin_fabsf(v.v[e]);  // NaN exactly when an entry is
+      packed = !any_lane(t != t);
+    }
+  }
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
     uint32_t w[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int e = 8 * c + 2 * k;
-      w[k] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(v.v[e]))) |
-             (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(v.v[e + 1]))) << 16);
+      if (packed) {
+        const F32x2 f = {v.v[e], v.v[e + 1]};
+        w[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, BF16x2));
+      } else {
+        w[k] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(v.v[e]))) |
+               (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(v.v[e + 1]))) << 16);
+      }
     }
     *reinterpret_cast<uint4*>(area + c * kDenseRowBytes + 16 * m) = make_uint4(w[0], w[1], w[2], w[3]);
   }
 }
+
+// With every count at most 4 the wavefront's (augmented) norms are at most
+// 16 theta18 < 49: the polynomial's intermediates stay below ~1e16 and the
+// squarings below ~e^49 (every partial sum is bounded by the product of the
+// factors' norms), so no entry overflows and no NaN can arise; a non-finite
+// matrix (count -1) is overwritten by the default NaN, which both roundings
+// write as 0x7FC0.
+constexpr int kNanFreeCount = 4;
 
 // Lanes below this one whose bit is set in `mask`.
 __device__ __forceinline__ int lanes_below(uint64_t mask) {
@@ -555,12 +585,13 @@ __global__ __launch_bounds__(64 * kP4Waves) __attribute__((amdgpu_waves_per_eu(P
       char* grp = slot + (id >> 6) * Slot::kGroup;
       const int m = id & 63;
       const PM<Pair> a = scaled<Pair>(matrix_at(grp, m), s, args.x.sign, args.g.sign);
-      squarings<Pair>(t18<Pair>(a), s, [&](const M4& out) { write_result_at<T>(grp, m, out); });
+      const bool nan_free = !any_lane(s > kNanFreeCount);
+      squarings<Pair>(t18<Pair>(a), s, [&](const M4& out) { write_result_at<T>(grp, m, out, nan_free); });
       if (s < 0) {  // rare: overwrite the result with NaN
         M4 nan;
 #pragma unroll
         for (int e = 0; e < 16; ++e) nan.v[e] = __builtin_nanf("");
-        write_result_at<T>(grp, m, nan);
+        write_result_at<T>(grp, m, nan, true);
       }
     }
     lds_order();

@@ -456,12 +456,15 @@ __device__ __forceinline__ Raw<T> read_tuples_at(const char* area, int m) {
 // software rounding for every non-NaN value) unless a lane of the wavefront
 // holds a NaN, which the software rounding writes as the reference's 0x7FC0
 // whatever its sign and payload.  `nan_free`: the caller knows no lane can.
+// FP16 always takes the packed conversion, which gives the scalar
+// conversion's bits for every input (NaNs included; measured on gfx950).
 typedef __bf16 BF16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 F16x2 __attribute__((ext_vector_type(2)));
 typedef float F32x2 __attribute__((ext_vector_type(2)));
 
 template <typename T>
 __device__ __forceinline__ void write_result_at(char* area, int m, const M4& v, bool nan_free) {
-  bool packed = false;
+  bool packed = __is_same(T, F16);
   if constexpr (__is_same(T, BF16)) {
     packed = nan_free;
     if (!packed) {
@@ -479,7 +482,11 @@ __device__ __forceinline__ void write_result_at(char* area, int m, const M4& v, 
       const int e = 8 * c + 2 * k;
       if (packed) {
         const F32x2 f = {v.v[e], v.v[e + 1]};
-        w[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, BF16x2));
+        if constexpr (__is_same(T, F16)) {
+          w[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, F16x2));
+        } else {
+          w[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, BF16x2));
+        }
       } else {
         w[k] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(v.v[e]))) |
                (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(v.v[e + 1]))) << 16);

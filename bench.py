@@ -131,25 +131,29 @@ def split_trials(total: int, trials: int) -> list[int]:
 
 
 def time_trials(torch, fn, steps: int, warmup: int, trials: int) -> dict:
-    """`warmup` untimed calls, then exactly `steps` timed calls split into trials; each trial is
-    bracketed by torch.cuda.synchronize() and timed with HIP events on the current stream (the one
-    the kernels launch on).  Returns the median and every trial's ms per call."""
+    """`warmup` untimed calls, then exactly `steps` timed calls bracketed by
+    torch.cuda.synchronize(), split into trials that are consecutive segments of that one run: a
+    HIP event on the current stream (the one the kernels launch on) between segments, no
+    synchronisation inside.  A trial thus measures the device time of its calls with the host
+    queueing ahead, as in a training loop, rather than the host's latency to the first launch on
+    an idle queue, which a synchronise per trial would add to every trial (~25 us on a slow host,
+    a quarter of a config-2 step over 4-step trials).  Returns the median and every trial's ms per
+    call; `mean_ms` is the whole run's."""
     stream = torch.cuda.current_stream()
     for _ in range(warmup):
         fn()
-    per_call = []
-    for size in split_trials(steps, trials):
-        torch.cuda.synchronize()
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        start.record(stream)
+    sizes = split_trials(steps, trials)
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(len(sizes) + 1)]
+    torch.cuda.synchronize()
+    events[0].record(stream)
+    for i, size in enumerate(sizes):
         for _ in range(size):
             fn()
-        end.record(stream)
-        torch.cuda.synchronize()
-        per_call.append(start.elapsed_time(end) / size)
+        events[i + 1].record(stream)
+    torch.cuda.synchronize()
+    per_call = [events[i].elapsed_time(events[i + 1]) / size for i, size in enumerate(sizes)]
     return {"median_ms": statistics.median(per_call), "trials_ms": per_call,
-            "mean_ms": sum(p * s for p, s in zip(per_call, split_trials(steps, trials))) / steps}
+            "mean_ms": events[0].elapsed_time(events[-1]) / steps}
 
 
 def settle(torch, fn, seconds: float) -> int:

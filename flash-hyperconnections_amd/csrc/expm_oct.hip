@@ -509,7 +509,7 @@ __global__ __launch_bounds__(64 * kOctWaves) __attribute__((amdgpu_waves_per_eu(
         S4 w;
 #pragma unroll
         for (int k = 0; k < 4; ++k) w[k] = from_f32<T>(row.v[k]);
-        *reinterpret_cast<S4*>(static_cast<S*>(args.out) + m * 64 + (4 * I + q) * 8 + 4 * J) = w;
+        __builtin_nontemporal_store(w, reinterpret_cast<S4*>(static_cast<S*>(args.out) + m * 64 + (4 * I + q) * 8 + 4 * J));
       }
     } else if (valid) {
       S* o = static_cast<S*>(args.out) + m * n * n;
@@ -517,7 +517,7 @@ __global__ __launch_bounds__(64 * kOctWaves) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 4 * I + r;
-        if (row < n && col < n) o[row * n + col] = from_f32<T>(out.v[r]);
+        if (row < n && col < n) __builtin_nontemporal_store(from_f32<T>(out.v[r]), &o[row * n + col]);
       }
     }
     if (valid && (lane & 15) == 0 && args.s_out) args.s_out[m] = s;

@@ -373,7 +373,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(3, 
           S4 w;
 #pragma unroll
           for (int c = 0; c < 4; ++c) w[c] = from_f32<T>(rows.v[4 * beta + c]);
-          *reinterpret_cast<S4*>(o + (4 * I + q) * 8 + 4 * J) = w;
+          __builtin_nontemporal_store(w, reinterpret_cast<S4*>(o + (4 * I + q) * 8 + 4 * J));
         }
       }
     } else if (valid) {
@@ -385,7 +385,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(3, 
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int row = 4 * I + r;
-          if (row < n && col < n) o[row * n + col] = from_f32<T>(res.v[4 * beta + r]);
+          if (row < n && col < n) __builtin_nontemporal_store(from_f32<T>(res.v[4 * beta + r]), &o[row * n + col]);
         }
       }
     }

@@ -324,13 +324,13 @@ __device__ __forceinline__ void store_tile(void* out, int64_t b, int n, int lane
   const int32_t lane_off = (C::row0(lane) * n + C::col(lane)) * es;
   if constexpr (Full) {
 #pragma unroll
-    for (int r = 0; r < C::R; ++r) ElemIO<T>::store(m.v[r], rs, lane_off + C::step(r) * P * es, 0);
+    for (int r = 0; r < C::R; ++r) ElemIO<T>::template store<kNontemporal>(m.v[r], rs, lane_off + C::step(r) * P * es, 0);
   } else {
     const bool col_ok = C::col(lane) < n;
 #pragma unroll
     for (int r = 0; r < C::R; ++r) {
       const bool ok = col_ok && C::row0(lane) + C::step(r) < n;
-      ElemIO<T>::store(m.v[r], rs, ok ? lane_off + C::step(r) * n * es : kOutOfRange, 0);
+      ElemIO<T>::template store<kNontemporal>(m.v[r], rs, ok ? lane_off + C::step(r) * n * es : kOutOfRange, 0);
     }
   }
 }

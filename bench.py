@@ -3,10 +3,10 @@
 Headline (``value``): BASELINE config 2 -- [1048576, 4, 4] FP32, entries N(0, 0.25^2),
 upstream gradient N(0, 1); one step = ``fh.matrix_exp`` forward plus
 ``torch.autograd.grad`` backward over the whole batch, inputs resident in HBM.
-Metric: matrices per second of forward + backward.  The K timed steps are split
-into >= 5 trials, each bracketed by a device synchronisation and timed with HIP
-events on the stream the kernels run on; ``ms_per_step`` is the median over the
-trials of the per-step time (every trial's time is kept in ``trials_ms``).  Before
+Metric: matrices per second of forward + backward.  The K timed steps run as one
+sequence bracketed by device synchronisations, split into >= 5 consecutive trials
+by HIP events on the stream the kernels run on; ``ms_per_step`` is the median over
+the trials of the per-step time (every trial's time is kept in ``trials_ms``).  Before
 its W warmup steps each config runs its step untimed for ``--settle`` seconds
 (default 0.3 s), so that the device has left its idle clocks when timing starts.
 
@@ -34,9 +34,11 @@ Also reported in the same JSON line:
   forward + backward, each fused kernel against the HBM roofline, beside the
   composed ``fh.matrix_exp(h) @ x`` on the same inputs;
 * ``reference_table`` -- the reference's own benchmark (N = 4, 8, 16, 32 at
-  B = 65,536 FP32, wall time per direct-API call) beside its published A100
-  figures; ``stock_gpu`` -- native torch.linalg.matrix_exp + autograd on this
-  GPU in the same sweep; ``small_batch_latency`` -- B = 1 wall time per call.
+  B = 65,536 FP32, wall time per direct-API call; with ``--sweep`` its whole
+  grid, B in {1, 128, 1024, 65536} x FP32/FP16/BF16, with seeds and input
+  hashes per row) beside its published A100 figures; ``stock_gpu`` -- native
+  torch.linalg.matrix_exp + autograd on this GPU in the same sweep;
+  ``small_batch_latency`` -- B = 1 wall time per call.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--trials T] [--settle S] [--skip-cpu]
                        [--only c2,...] [--extras] [--sweep]
@@ -627,6 +629,7 @@ def reference_table(torch, fh, device, sizes=(4, 8, 16, 32), batches=(65536,), d
                 torch.manual_seed(seed)
                 a = (torch.randn(batch, n, n, device=device) * 0.1).to(dtype)
                 g = (torch.randn(batch, n, n, device=device) * 0.2).to(dtype)
+                a_hash, g_hash = sha256(a), sha256(g)  # the whole tensors, as the reference records
                 for mode in ("forward", "forward_backward"):
                     x = a.detach().requires_grad_(mode == "forward_backward")
                     impls = {"flash_hypercons": fh.matrix_exp, "stock": native}
@@ -652,7 +655,8 @@ def reference_table(torch, fh, device, sizes=(4, 8, 16, 32), batches=(65536,), d
                             times[k].append((time.perf_counter() - t0) * 1e6 / repeat)
                     us = statistics.median(times["flash_hypercons"])
                     stock = statistics.median(times["stock"])
-                    row = {"n": n, "batch": batch, "dtype": dname, "mode": mode, "median_us": us,
+                    row = {"n": n, "batch": batch, "dtype": dname, "mode": mode, "seed": seed,
+                           "input_sha256": a_hash, "grad_sha256": g_hash, "median_us": us,
                            "matrices_per_s": batch / us * 1e6, "stock_gpu_us": stock, "speedup_vs_stock": stock / us,
                            "trials_us": times["flash_hypercons"], "stock_trials_us": times["stock"]}
                     ref = REFERENCE_A100_US.get((n, mode)) if (dname == "f32" and batch == 65536) else None

@@ -7,10 +7,10 @@
 // per-matrix scalar work (norm, squaring count, scaling) is done once per
 // matrix rather than once per row.
 //
-// What bounds it on gfx950 (measured): a wave64 FP32 VALU instruction issues
-// every ~4.1 cycles per SIMD whatever the occupancy (16 lanes per clock,
-// unpacked), FP32 MFMA does not overlap VALU work on the same SIMD, and a
-// VALU instruction with 16 or fewer active lanes costs ~5x a full one.  So the
+// What bounds it on gfx950 (measured): wave64 FP32 VALU instructions issue
+// every ~2.5-3 cycles per SIMD with two or more wavefronts on it (~5 cycles
+// with one), FP32 MFMA does not overlap VALU work on the same SIMD, and a VALU
+// instruction with 16 or fewer active lanes costs ~5x a full one.  So the
 // kernel is shaped to issue as few VALU instructions as possible, all with
 // full exec masks:
 //  * operand classes (row / column vectors, dense 64-matrix blocks) are

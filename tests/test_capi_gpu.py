@@ -1,4 +1,4 @@
-"""The C ABI launched on the GPU the way INTEGRATION.md tells a caller to bind it.
+"""The C ABI launched on the GPU the way a caller of include/flash_hypercons.h binds it.
 
 ctypes loads libflash_hypercons_hip.so directly (no torch extension in the
 path), passes device pointers, element strides, the negation flag, the dtype

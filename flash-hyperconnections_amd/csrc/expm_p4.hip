@@ -174,7 +174,7 @@ __device__ __forceinline__ void store_group(__amdgpu_buffer_rsrc_t out, int32_t 
     const float v3 = tile[mat * kStageStride + e + 3];
     if constexpr (sizeof(typename T::storage) == 4) {
       const U32x4 w = {__float_as_uint(v0), __float_as_uint(v1), __float_as_uint(v2), __float_as_uint(v3)};
-      __builtin_amdgcn_raw_buffer_store_b128(w, out, 4 * f, group_bytes, kNontemporal);
+      __builtin_amdgcn_raw_buffer_store_b128(w, out, group_bytes + 4 * f, kStoreSOffset, kNontemporal);
     } else {
       const uint32_t lo = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(v0))) |
                           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(v1))) << 16);
@@ -609,7 +609,8 @@ __global__ __launch_bounds__(64 * kP4Waves) __attribute__((amdgpu_waves_per_eu(P
       for (int c = 0; c < C; ++c) {
         const uint4 v = *reinterpret_cast<const uint4*>(slot + h * Slot::kGroup + c * kDenseRowBytes + 16 * lane);
         const U32x4 w = {v.x, v.y, v.z, v.w};
-        __builtin_amdgcn_raw_buffer_store_b128(w, out_rs, 16 * (C * lane + c), (2 * q + h) * kGroupBytes, kNontemporal);
+        __builtin_amdgcn_raw_buffer_store_b128(w, out_rs, (2 * q + h) * kGroupBytes + 16 * (C * lane + c),
+                                               kStoreSOffset, kNontemporal);
       }
     lds_order();
     which ^= 1;

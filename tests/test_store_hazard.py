@@ -12,6 +12,7 @@ against the instruction after it.
 import re
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 import pytest
@@ -58,12 +59,17 @@ def test_scanner_flags_an_overwrite():
     assert not overwritten_stores("buffer_store_dwordx2 v[0:1], v69, s[48:51], 0 offen\nv_mov_b32 v0, 1\n")
 
 
-@pytest.mark.parametrize("source", [s for s in fh_build.KERNEL_SOURCES if s.endswith(".hip")])
-def test_kernels_keep_store_data_until_read(source, tmp_path):
-    out = tmp_path / (source + ".s")
+def _assembly(source: str, out: Path) -> str:
     flags = [f for f in fh_build.HIP_FLAGS if f != "-fPIC"]
     proc = subprocess.run([fh_build.HIPCC, *flags, "--cuda-device-only", "-S", str(fh_build.CSRC / source), "-o",
                            str(out)], capture_output=True, text=True)
-    assert proc.returncode == 0, proc.stderr[-2000:]
-    found = overwritten_stores(out.read_text())
+    assert proc.returncode == 0, f"{source}: {proc.stderr[-2000:]}"
+    return out.read_text()
+
+
+def test_kernels_keep_store_data_until_read(tmp_path):
+    sources = [s for s in fh_build.KERNEL_SOURCES if s.endswith(".hip")]
+    with ThreadPoolExecutor(max_workers=min(8, len(sources))) as pool:  # one hipcc process per source
+        asm = dict(zip(sources, pool.map(lambda s: _assembly(s, tmp_path / (s + ".s")), sources)))
+    found = [f"{src}: {hit}" for src, text in asm.items() for hit in overwritten_stores(text)]
     assert not found, "\n".join(found[:5])

@@ -308,36 +308,6 @@ __global__ __launch_bounds__(64 * kP4Waves) __attribute__((amdgpu_waves_per_eu(P
 // 16 l: the padded, conflict-free layout each lane reads its own matrix from.
 // A slot is reused for the group's staged results once its inputs are read.
 
-// Buffer-to-LDS load of 16 bytes per lane: lane l's bytes land at LDS byte
-// address lds_addr + 16 l.  Written as assembly so that the compiler's wait
-// insertion does not make every LDS read wait for these loads (it cannot tell
-// the two slots apart); wait_vm<N>() orders them instead.  `rsrc` is the buffer
-// resource as four words.
-__device__ __forceinline__ void lds_load16(U32x4 rsrc, uint32_t lds_addr, int32_t voff, int32_t soff) {
-  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" : : "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds_addr)
-               : "memory");
-}
-
-__device__ __forceinline__ uint32_t lds_address(const void* p) {
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
-}
-
-// Resource words of make_rsrc(base, 0x7FFFFFFF): base address, stride 0,
-// num_records, and the same fourth word.
-__device__ __forceinline__ U32x4 rsrc_words(const void* base) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  return U32x4{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32) & 0xFFFFu, 0x7FFFFFFFu, 0x00020000u};
-}
-
-// s_waitcnt vmcnt(N): at most N vector memory operations of this wavefront
-// outstanding.  Loads complete in issue order, so this waits for every load
-// issued before the last N loads.
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 16, "vmcnt immediate");
-  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
-}
-
 // One operand's group block into LDS rows c * 1040 (the dense_to_lane layout).
 template <typename T>
 __device__ __forceinline__ void load_group_to_lds(U32x4 rs, uint32_t lds_addr, int32_t group_bytes, int lane) {
@@ -503,12 +473,6 @@ __device__ __forceinline__ void write_result_at(char* area, int m, const M4& v, 
 // matrix (count -1) is overwritten by the default NaN, which both roundings
 // write as 0x7FC0.
 constexpr int kNanFreeCount = 4;
-
-// Lanes below this one whose bit is set in `mask`.
-__device__ __forceinline__ int lanes_below(uint64_t mask) {
-  return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
-                                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u)));
-}
 
 // Persistent kernel over batches of two full groups of a 2-byte dense batch
 // (n == 4): batch q is groups 2q and 2q + 1.

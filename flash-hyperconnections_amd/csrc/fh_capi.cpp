@@ -41,16 +41,17 @@ fh::Operand make_operand(const void* data, const int64_t strides[3], int neg, in
   if (n == 4 || n == 8) {
     // Every row (or column) of the matrix is made of aligned 4-element
     // vectors when its elements are adjacent and every matrix/row (column)
-    // start keeps the vector alignment; for n == 4 the 64 matrices of a group
-    // are one contiguous block (`dense`) when they are packed as well.
+    // start keeps the vector alignment; consecutive matrices are one
+    // contiguous block (`dense`) when they are packed as well.
     const int64_t vbytes = 4 * element_size(dtype);
     const bool base_ok = aligned(data, vbytes) && strides[0] % 4 == 0;
+    const bool packed = strides[0] == n * n && aligned(data, 16);
     if (base_ok && strides[2] == 1 && strides[1] % 4 == 0) {
       op.vec = fh::kVecRows;
-      op.dense = n == 4 && strides[0] == 16 && strides[1] == 4 && aligned(data, 16);
+      op.dense = packed && strides[1] == n;
     } else if (base_ok && strides[1] == 1 && strides[2] % 4 == 0) {
       op.vec = fh::kVecCols;
-      op.dense = n == 4 && strides[0] == 16 && strides[2] == 4 && aligned(data, 16);
+      op.dense = packed && strides[2] == n;
     }
   }
   return op;

@@ -46,12 +46,12 @@ struct F16 {
 
 // One [batch, n, n] operand read through element strides.  `sign` is -1 for
 // a lazily negated tensor view and +1 otherwise (multiplying by it is exact).
-// `vec` tells the P == 4 kernel that every row (kVecRows: sc == 1) or every
-// column (kVecCols: sr == 1) of a 4 x 4 matrix is one aligned 4-element
-// vector; the host sets it only when n == 4 and the alignment holds.
-// `dense` adds that the matrices themselves are packed (16 elements apart,
-// rows or columns 4 apart), so 64 consecutive matrices are one contiguous,
-// 16-byte aligned block.
+// `vec` tells the P == 4 and P == 8 kernels that every row (kVecRows:
+// sc == 1) or every column (kVecCols: sr == 1) of a 4 x 4 or 8 x 8 matrix is
+// made of aligned 4-element vectors; the host sets it only when n is 4 or 8
+// and the alignment holds.  `dense` adds that the matrices themselves are
+// packed (n * n elements apart, rows or columns n apart), so consecutive
+// matrices are one contiguous, 16-byte aligned block.
 constexpr int kVecNone = 0;
 constexpr int kVecRows = 1;
 constexpr int kVecCols = 2;
@@ -232,5 +232,48 @@ struct ElemIO<BF16> {
 };
 
 __device__ __forceinline__ bool finite_f32(float v) { return __builtin_isfinite(v); }
+
+// ---- buffer-to-LDS loads ------------------------------------------------------
+
+typedef uint32_t U32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer-to-LDS load of 16 bytes per lane: lane l's bytes land at LDS byte
+// address lds_addr + 16 l.  Written as assembly so that the compiler's wait
+// insertion does not make every LDS read wait for these loads (it cannot tell
+// LDS areas apart); wait_vm<N>() orders them instead.  `rsrc` is the buffer
+// resource as four words.
+__device__ __forceinline__ void lds_load16(U32x4 rsrc, uint32_t lds_addr, int32_t voff, int32_t soff) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" : : "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds_addr)
+               : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
+}
+
+// Resource words of make_rsrc(base, 0x7FFFFFFF): base address, stride 0,
+// num_records, and the same fourth word.
+__device__ __forceinline__ U32x4 rsrc_words(const void* base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return U32x4{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32) & 0xFFFFu, 0x7FFFFFFFu, 0x00020000u};
+}
+
+// s_waitcnt vmcnt(N): at most N vector memory operations of this wavefront
+// outstanding.  Loads complete in issue order, so this waits for every load
+// issued before the last N loads.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 16, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
+
+// s_waitcnt lgkmcnt(0): every LDS access this wavefront issued is complete.
+__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Lanes below this one whose bit is set in `mask`.
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+  return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u)));
+}
 
 }  // namespace fh

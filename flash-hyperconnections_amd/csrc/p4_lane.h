@@ -16,7 +16,6 @@
 namespace fh {
 namespace p4 {
 
-typedef uint32_t U32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t U32x2 __attribute__((ext_vector_type(2)));
 
 struct M4 {

@@ -197,6 +197,44 @@ def test_p4_count_ordered_batches_bitwise(batch, dtype, backward):
         assert bool((out.view(torch.int16)[nan] == 0x7FC0).all())
 
 
+@pytest.mark.parametrize("layout", ["rows", "cols"])
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("batch", [32, 3 * 32, 5 * 32 + 17, 4096 + 21])
+def test_p8_count_ordered_batches_bitwise(batch, dtype, layout):
+    """Dense n = 8 forward batches run in pairs of 16-matrix units ordered by squaring count,
+    with the count taken from the row layout for row-major operands.  Cases: whole pairs, a
+    partial last pair (one full and one partial unit), both dense layouts, and inside the full
+    pairs non-finite matrices (s = -1), counts above 127 (entries near the dtype's maximum),
+    counts from 0 to ~7, and the squaring-boundary fixture's matrices, whose counts only the
+    exact FP64 norm decides.  Every matrix must match the oracle bit for bit and report the
+    oracle's count."""
+    from pathlib import Path
+
+    import numpy as np
+
+    fixture = np.load(Path(__file__).resolve().parent / "golden" / "s_boundaries.npz")
+    a, _ = scaled_inputs(batch, 8, torch.float32, seed=batch + 31 * DTYPES.index(dtype), low=-4.0, high=2.0)
+    at = torch.arange(fixture["x8"].shape[0]) * 3 + 1
+    a[at] = torch.from_numpy(fixture["x8"])
+    a[2, 1, 6] = float("nan")
+    a[6, 7, 7] = float("inf")
+    a[batch - 40 if batch > 64 else 12, 0, 3] = -float("inf")
+    big = {torch.float32: 3.0e38, torch.bfloat16: 3.0e38, torch.float16: 6.0e4}[dtype]
+    a[9] = torch.full((8, 8), big)
+    a[17, :, 5] = -big
+    x = _laid_out(a.to(dtype).cuda(), layout)
+    out, s = run_kernel(x, None, AUTO)
+    exp_out, exp_s = oracle_result(x, None)
+    assert torch.equal(s.cpu(), exp_s)
+    if dtype == torch.float32:  # the boundary matrices keep their counts only in FP32
+        assert exp_s[at].tolist() == fixture["s8"].tolist()
+    if dtype != torch.float16:
+        assert int(exp_s.max()) > 127
+    assert int((exp_s < 0).sum()) >= 3
+    ok, bad = same_values(out, exp_out)
+    assert ok, f"{bad} elements differ from the oracle"
+
+
 @pytest.mark.parametrize("n", [4, 8, 16, 32])
 def test_nonfinite_rule_matches_oracle(n):
     a = torch.zeros(5, n, n, device="cuda")

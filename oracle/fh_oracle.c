@@ -29,6 +29,14 @@
  *   t = c0*I; t = fmaf(c1,A,t); t = fmaf(c2,A2,t); t = fmaf(c3,A3,t); t = fmaf(c6,A6,t)
  * (U blocks start from c1*A).  Build with -ffp-contract=off so that the
  * compiler adds no contraction of its own.
+ *
+ * Parity unpinned: that contraction order.  nvcc may equally contract the
+ * diagonal term first (fmaf(c0, I, c1*A)), which rounds differently on the
+ * diagonal of B3/B4; no fixture of the reference tells the two apart and nvcc
+ * is absent here.  fho_set_combine_contraction(1) switches this restatement
+ * to that order, and tests/test_oracle.py bounds the difference between the
+ * two (one rounding, amplified by the squarings).  Likewise unobservable here:
+ * CUDA's log2 inside the 2^-40 band above a power of two where s needs it.
  */
 #include <math.h>
 #include <stdint.h>

@@ -1,11 +1,13 @@
 """Parity at BASELINE.json's full sizes, over every matrix (GPU).
 
-For configs 2-5 (and config 5's shape in FP32) the seeded inputs of bench.py
-run one forward + backward step through the public surface; then, for every
-matrix of the batch and both directions (tests/fullsize.py):
+For configs 2-5 (and config 5's shape in FP32, and bench.py's P = 8 line,
+[262144, 8, 8] FP32) the seeded inputs of bench.py run one forward + backward
+step through the public surface; then, for every matrix of the batch and both
+directions (tests/fullsize.py):
 
 * the squaring count s equals the CPU restatement's (0 mismatches);
-* at n = 4 (configs 2, 3) every result is bit-identical to the restatement;
+* at n = 4 (configs 2, 3) and n = 8 (the P = 8 line) every result is
+  bit-identical to the restatement;
 * no more matrices break the strict north-star rule than for the reference's
   own arithmetic (the restatement) on the same inputs, and in FP32 the mean
   error is within 1.05x of the restatement's;
@@ -45,7 +47,7 @@ def _step(name):
     return x.detach(), g, y.detach(), grad
 
 
-@pytest.mark.parametrize("name", ["c2", "c3", "c4", "c5", "c5f32"])
+@pytest.mark.parametrize("name", ["c2", "c3", "c4", "c5", "c5f32", "p8"])
 def test_every_matrix_of_baseline_config(name):
     x, g, y, grad = _step(name)
     report = workload_parity(x, g, y, grad)

@@ -398,11 +398,10 @@ struct UnitRaw {
 
 // ---- kernel -----------------------------------------------------------------
 
-// Persistent kernel: each wavefront walks 4-matrix units with a grid stride
-// and issues the next unit's loads before computing the current one.  Four
-// wavefronts per SIMD (at most 128 VGPRs): the element-wise Frechet variant
-// (n < 8) would take 133 and run three; held to 128 it spills 16-32 bytes and
-// is 6% faster at [262144, 6, 6].
+// One 4-matrix unit per wavefront (beyond 2^22 units wavefronts walk them
+// with a grid stride), loaded at the unit's start: the hardware starts a
+// workgroup as another retires.  Four wavefronts per SIMD (at most 128
+// VGPRs).
 template <typename T, bool Pair, int XL, int GL>
 __global__ __launch_bounds__(64 * kOctWaves) __attribute__((amdgpu_waves_per_eu(4, 8))) void expm_oct_kernel(ExpmArgs args) {
   using S = typename T::storage;
@@ -431,15 +430,13 @@ __global__ __launch_bounds__(64 * kOctWaves) __attribute__((amdgpu_waves_per_eu(
     return r;
   };
 
-  UnitRaw<T, Pair, XL, GL> next;
-  if (unit < units) next = load_unit(unit);
   for (; unit < units; unit += stride) {
     const int64_t m = unit * kOctUnit + slot;
     const bool valid = m < args.batch;
+    const UnitRaw<T, Pair, XL, GL> raw = load_unit(unit);
     PQ<Pair> lx;  // as loaded: R layout for kVecRows, C layout otherwise
-    lx.d = to_q<T>(next.x);
-    if constexpr (Pair) lx.u = to_q<T>(next.g);
-    if (unit + stride < units) next = load_unit(unit + stride);
+    lx.d = to_q<T>(raw.x);
+    if constexpr (Pair) lx.u = to_q<T>(raw.g);
 
     // X (and G) in the C layout and as whole rows.
     PQ<Pair> ac;
@@ -526,12 +523,9 @@ __global__ __launch_bounds__(64 * kOctWaves) __attribute__((amdgpu_waves_per_eu(
 
 template <typename T, bool Pair, int XL, int GL>
 hipError_t launch_oct_l(const ExpmArgs& args, hipStream_t stream) {
-  // Persistent grid: as many workgroups as the device keeps resident at once.
-  static const int64_t resident =
-      resident_blocks(reinterpret_cast<const void*>(&expm_oct_kernel<T, Pair, XL, GL>), 64 * kOctWaves);
   const int64_t units = (args.batch + kOctUnit - 1) / kOctUnit;
   int64_t grid = (units + kOctWaves - 1) / kOctWaves;
-  if (grid > resident) grid = resident;
+  if (grid > (int64_t{1} << 20)) grid = int64_t{1} << 20;
   hipLaunchKernelGGL((expm_oct_kernel<T, Pair, XL, GL>), dim3(static_cast<unsigned>(grid)), dim3(64 * kOctWaves), 0,
                      stream, args);
   return hipGetLastError();

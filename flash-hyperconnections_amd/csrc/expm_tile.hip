@@ -22,8 +22,11 @@
 // * loads and stores go through buffer resources: one per-lane offset fixed
 //   for the whole kernel, the per-VGPR row offsets in scalar registers and
 //   the matrix base in the descriptor, so addressing costs no VALU;
-// * the next matrix's storage bits are prefetched into registers and only
-//   converted when its turn comes, so the prefetch never stalls;
+// * one matrix per wavefront and no prefetch of a next one: against a
+//   persistent grid that prefetched the next matrix's storage bits, the
+//   forward at config 5 ran 151.3 -> 143.7 us, and without the prefetch's
+//   registers no Frechet variant spills and the P = 16 one runs six
+//   wavefronts per SIMD instead of five;
 // * s comes from an FP32 estimate of the norm (a few adds and a cross-lane
 //   maximum) whenever that estimate decides it exactly; the FP64 sequential
 //   column sums of the reference run only near a squaring boundary or for
@@ -419,11 +422,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kTileWaves<P
   const TileSrc sg = make_src<T, P>(args.g, GL, n, lane);
 
   int64_t b = blockIdx.x;
-  RawTile<T, P> nx, ng;
-  if (b < args.batch) {
-    nx = load_raw<T, P, Full>(sx, b, n, lane);
-    if constexpr (Pair) ng = load_raw<T, P, Full>(sg, b, n, lane);
-  }
   const int dreg_lane = C::diag_reg(lane);
   Ident<P> id_lane;
   if constexpr (P == 16) {
@@ -442,9 +440,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kTileWaves<P
       asm volatile("" : "+v"(dreg));
       id = make_ident<P>(dreg);
     }
-    const Tm<P> lx = to_tile<T, P>(nx);
-    Tm<P> lg;
-    if constexpr (Pair) lg = to_tile<T, P>(ng);
     // n < P = 32: the per-VGPR bounds predicates and offsets are formed
     // afresh for each matrix from an opaque copy of the lane's offsets, so
     // that they are not kept live across the loop (2R-3R registers these
@@ -454,10 +449,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kTileWaves<P
     if constexpr (!Full && P == 32) {
       asm volatile("" : "+v"(sxm.lane_off), "+v"(sgm.lane_off), "+v"(lane_m));
     }
-    if (b + gridDim.x < args.batch) {
-      nx = load_raw<T, P, Full>(sxm, b + gridDim.x, n, lane_m);
-      if constexpr (Pair) ng = load_raw<T, P, Full>(sgm, b + gridDim.x, n, lane_m);
-    }
+    const Tm<P> lx = to_tile<T, P>(load_raw<T, P, Full>(sxm, b, n, lane_m));
+    Tm<P> lg;
+    if constexpr (Pair) lg = to_tile<T, P>(load_raw<T, P, Full>(sgm, b, n, lane_m));
 
     // Both layouts of X (and G): the loaded one and its LDS transpose.
     PTm<P, Pair> a, at;
@@ -525,13 +519,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kTileWaves<P
 
 template <typename T, int P, bool Pair, int XL, int GL, bool Full>
 hipError_t launch_tile_l(const ExpmArgs& args, hipStream_t stream) {
-  // The Frechet kernel walks the batch on a persistent grid (its prefetch hides
-  // the next matrix's loads); the forward takes one matrix per wavefront and
-  // lets the hardware start a workgroup as another retires (C5 forward 151.3
-  // -> 143.7 us, same process, alternating), up to 2^24 workgroups.
-  static const int64_t resident =
-      resident_blocks(reinterpret_cast<const void*>(&expm_tile_kernel<T, P, Pair, XL, GL, Full>), 64);
-  const int64_t cap = Pair ? resident : int64_t{1} << 24;
+  // One matrix per wavefront (up to 2^24 workgroups, beyond which wavefronts
+  // walk the batch with a grid stride): the hardware starts a workgroup as
+  // another retires.
+  const int64_t cap = int64_t{1} << 24;
   const int64_t grid = args.batch < cap ? args.batch : cap;
   hipLaunchKernelGGL((expm_tile_kernel<T, P, Pair, XL, GL, Full>), dim3(static_cast<unsigned>(grid)), dim3(64), 0,
                      stream, args);

@@ -22,7 +22,8 @@
 // * loads and stores go through buffer resources: one per-lane offset fixed
 //   for the whole kernel, the per-VGPR row offsets in scalar registers and
 //   the matrix base in the descriptor, so addressing costs no VALU;
-// * one matrix per wavefront and no prefetch of a next one: against a
+// * no prefetch of a next matrix, on a grid of one wavefront per matrix
+//   (P = 32) or four times the resident workgroups (P = 16): against a
 //   persistent grid that prefetched the next matrix's storage bits, the
 //   forward at config 5 ran 151.3 -> 143.7 us, and without the prefetch's
 //   registers no Frechet variant spills and the P = 16 one runs six
@@ -519,10 +520,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kTileWaves<P
 
 template <typename T, int P, bool Pair, int XL, int GL, bool Full>
 hipError_t launch_tile_l(const ExpmArgs& args, hipStream_t stream) {
-  // One matrix per wavefront (up to 2^24 workgroups, beyond which wavefronts
-  // walk the batch with a grid stride): the hardware starts a workgroup as
-  // another retires.
-  const int64_t cap = int64_t{1} << 24;
+  // P = 32: one matrix per wavefront (up to 2^24 workgroups, beyond which
+  // wavefronts walk the batch with a grid stride), the hardware starting a
+  // workgroup as another retires.  P = 16: four times the resident workgroups,
+  // each walking two or three matrices, which spreads the per-wavefront setup
+  // (C4 step 158.1 -> 155.0 and 159.2 -> 154.9 us against one matrix per
+  // wavefront; 2x, 8x and 16x resident measured slower; P = 32 at 2x and 4x
+  // slower than one per wavefront).
+  static const int64_t resident =
+      resident_blocks(reinterpret_cast<const void*>(&expm_tile_kernel<T, P, Pair, XL, GL, Full>), 64);
+  const int64_t cap = P == 16 ? 4 * resident : int64_t{1} << 24;
   const int64_t grid = args.batch < cap ? args.batch : cap;
   hipLaunchKernelGGL((expm_tile_kernel<T, P, Pair, XL, GL, Full>), dim3(static_cast<unsigned>(grid)), dim3(64), 0,
                      stream, args);

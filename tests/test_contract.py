@@ -352,6 +352,31 @@ def test_operand_spanning_more_than_2gib(n):
     del storage, a
 
 
+@pytest.mark.parametrize("n", [4, 8])
+def test_dense_batch_larger_than_2gib(n):
+    """A packed batch of more than 2 GiB: the buffer-to-LDS (P = 4) and count-ordered (P = 8)
+    kernels address it with 32-bit offsets, so the launcher takes the 64-bit-indexed kernels.
+    Sampled matrices (the first, those around byte 2^31, the last, and random ones) must be
+    the bits the same matrices give in a small batch and the oracle's, forward and Frechet."""
+    batch = (1 << 31) // (4 * n * n) + 3
+    gen = torch.Generator(device="cuda").manual_seed(n)
+    x = torch.randn(batch, n, n, device="cuda", generator=gen) * 0.3
+    g = torch.randn(batch, n, n, device="cuda", generator=gen)
+    edge = (1 << 31) // (4 * n * n)
+    idx = torch.cat((torch.tensor([0, edge - 2, edge - 1, edge, edge + 1, batch - 1]),
+                     torch.randint(0, batch, (250,), generator=torch.Generator().manual_seed(n)))).unique().cuda()
+    for y, small, direction in ((EXP(x), EXP(x[idx]), None), (FRECHET(x.mT, g), FRECHET(x[idx].mT, g[idx]), g)):
+        assert torch.equal(y[idx], small)
+        if direction is None:
+            want, _ = oracle.torch_matrix_exp(x[idx].cpu())
+        else:
+            want, _ = oracle.torch_frechet(x[idx].mT.cpu(), direction[idx].cpu())
+        assert torch.equal(small.cpu(), want)
+        del y
+    del x, g
+    torch.cuda.empty_cache()
+
+
 def test_invalid_direct_calls_raise_reference_messages():
     with pytest.raises(RuntimeError, match="expected a strided CUDA"):
         EXP(torch.randn(2, 33, 33, device="cuda"))

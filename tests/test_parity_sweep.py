@@ -1,0 +1,115 @@
+"""A seeded sweep over the operator's input space against the CPU oracle (GPU).
+
+300 cases, each drawing n (2..32), dtype, batch size (log-uniform, up to 20,000 matrices
+for n <= 8), the operand layout (contiguous, transposed, lazily negated, padded rows,
+stride-0 batch), the direction (forward, or Frechet with its own layout) and the spread of
+1-norms (10^lo..10^hi, lo in [-4, 0], hi in [0, 2.5]).  For every matrix:
+
+* the squaring count equals the oracle's;
+* n <= 8: the result is bit-identical to the oracle's (NaN where it has NaN);
+* n >= 9 (MFMA tiles, which sum a product's k terms in another order): every element
+  within 2^s times 1e-4 (FP32) or 1e-3, at least 0.02 (FP16/BF16) of the matrix's largest
+  oracle entry, and the same NaN pattern wherever the oracle's result is finite.  Where it
+  is not, the exact result lies beyond FP32's range (norms of several hundred) and which
+  non-finite value each order produces is an artefact of that order.
+"""
+
+import math
+import random
+
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+LAYOUTS = ["contiguous", "transposed", "negated", "padded", "expanded"]
+
+
+def _laid_out(v, kind):
+    if kind == "contiguous":
+        return v.contiguous()
+    if kind == "transposed":
+        return v.mT.contiguous().mT
+    if kind == "negated":
+        return torch._neg_view((-v).contiguous())
+    if kind == "padded":
+        b, n, _ = v.shape
+        p = torch.zeros(b, n, n + 3, dtype=v.dtype, device=v.device)
+        p[:, :, :n] = v
+        return p[:, :, :n]
+    return v[:1].expand(v.shape[0], -1, -1)
+
+
+def _case(rng):
+    n = rng.randint(2, 32)
+    dtype = rng.choice(DTYPES)
+    bmax = 20000 if n <= 8 else (3000 if n <= 16 else 400)
+    batch = max(1, int(math.exp(rng.uniform(0, math.log(bmax)))))
+    kind = rng.choice(LAYOUTS)
+    backward = rng.random() < 0.5
+    lo, hi = rng.uniform(-4, 0), rng.uniform(0, 2.5)
+    seed = rng.randrange(1 << 30)
+    gkind = rng.choice(["contiguous", "transposed", "padded"]) if backward and rng.random() < 0.5 else None
+    return n, dtype, batch, kind, backward, lo, hi, seed, gkind
+
+
+def _inputs(n, dtype, batch, kind, backward, lo, hi, seed, gkind):
+    gen = torch.Generator().manual_seed(seed)
+    base = torch.randn(batch, n, n, generator=gen, dtype=torch.float64)
+    base = base / torch.linalg.matrix_norm(base, ord=1)[:, None, None]
+    scale = 10 ** torch.empty(batch, dtype=torch.float64).uniform_(lo, hi, generator=gen)
+    if dtype == torch.float16:
+        scale = scale.clamp(max=2e3)
+    x = _laid_out((base * scale[:, None, None]).to(dtype).cuda(), kind)
+    g = None
+    if backward:
+        g = torch.randn(batch, n, n, generator=gen).to(dtype).cuda()
+        if gkind:
+            g = _laid_out(g, gkind)
+    return x, g
+
+
+def _mismatches(out, s, want, want_s, n, dtype):
+    why = []
+    if not torch.equal(s.cpu(), want_s):
+        why.append(f"{int((s.cpu() != want_s).sum())} squaring counts differ")
+    o, w = out.cpu().double(), want.double()
+    if n <= 8:
+        equal = (o == w) | (o.isnan() & w.isnan())
+        if not bool(equal.all()):
+            why.append(f"{int((~equal).sum())} elements differ in bits")
+        return why
+    finite = torch.isfinite(w).flatten(1).all(1)
+    wf, of = w[finite], o[finite]
+    scale = wf.abs().flatten(1).amax(1).clamp(min=1e-30)[:, None, None]
+    tol = (1e-4 if dtype == torch.float32 else 1e-3) * 2.0 ** want_s[finite].clamp(min=0).double()[:, None, None]
+    if dtype != torch.float32:
+        tol = tol.clamp(min=0.02)
+    over = ((of - wf).abs() / scale > tol) | of.isnan()
+    if bool(over.any()):
+        why.append(f"{int(over.flatten(1).any(1).sum())} finite-result matrices outside the tolerance")
+    return why
+
+
+def test_seeded_sweep_matches_the_oracle():
+    import flash_hypercons  # noqa: F401
+
+    debug = torch.ops.flash_hypercons._expm_debug
+    rng = random.Random(7)
+    failures = []
+    for i in range(300):
+        case = _case(rng)
+        n, dtype = case[0], case[1]
+        x, g = _inputs(*case)
+        out, s = debug(x, g, 0)
+        if g is None:
+            want, want_s = oracle.torch_matrix_exp(x.cpu())
+        else:
+            want, want_s = oracle.torch_frechet(x.cpu(), g.cpu())
+        why = _mismatches(out, s, want, want_s, n, dtype)
+        if why:
+            failures.append(f"case {i} {case}: {'; '.join(why)}")
+    assert not failures, "\n".join(failures[:5])

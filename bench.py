@@ -789,7 +789,7 @@ def main() -> int:
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": profiled_traffic("expm_p4_frechet_c2_f32"),
             "traffic_source": "profiles/expm_p4_c2_hbm_traffic.md (FETCH_SIZE, WRITE_SIZE; copy-calibrated)",
-            "kernel": "expm_p4_kernel<F32, Pair=true> (Frechet backward, P=4)",
+            "kernel": "expm_p4_dma_kernel<F32, true, 2, 1> (Frechet backward, P=4, buffer-to-LDS loads)",
             "algorithmic_bytes_per_launch": bytes_bwd,
             "median_launch_ms": head["ms_bwd_kernel"],
             "launch_trials_ms": head["ms_bwd_trials"],

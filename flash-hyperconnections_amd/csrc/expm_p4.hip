@@ -303,7 +303,9 @@ __global__ __launch_bounds__(64 * kP4Waves) __attribute__((amdgpu_waves_per_eu(P
 //
 // For dense operands the groups go from HBM to the wavefront's LDS with
 // buffer-to-LDS loads, no registers involved, a group ahead in a two-slot
-// ring.  Load instruction c of a group has lane l fetch tuple C l + c of the
+// ring when a wavefront walks several groups (the Frechet kernel's persistent
+// grid; the forward's grid gives each wavefront one group, so its second slot
+// stays idle).  Load instruction c of a group has lane l fetch tuple C l + c of the
 // 64-matrix block, so that it writes LDS row c with matrix l's tuple c at byte
 // 16 l: the padded, conflict-free layout each lane reads its own matrix from.
 // A slot is reused for the group's staged results once its inputs are read.

@@ -10,7 +10,13 @@ the trials of the per-step time (every trial's time is kept in ``trials_ms``).  
 its W warmup steps each config runs its step untimed for ``--settle`` seconds
 (default 0.3 s), so that the device has left its idle clocks when timing starts.
 
-Also reported in the same JSON line:
+stdout carries ONE compact JSON line (well under 8 KB: the required keys, ``roofline``,
+``cpu_baseline``, ``cold_step`` and one short summary per config and per parity gate); the
+full report -- every field below with every trial -- goes to stderr and to ``--report``
+(default gpurun_out/bench_report.json), as the reference's benchmark writes its report to a
+file (benchmarks/matrix_exp.py:119-125).
+
+Reported (in full in the report, summarised in the line):
 * ``roofline`` -- the dominant kernel of that step (the P = 4 Frechet kernel):
   algorithmic bytes per launch / its median launch time (HIP events around
   back-to-back launches, same trial split) against MI355X's 8 TB/s;
@@ -41,7 +47,7 @@ Also reported in the same JSON line:
   ``small_batch_latency`` -- B = 1 wall time per call.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--trials T] [--settle S] [--skip-cpu]
-                       [--only c2,...] [--extras] [--sweep]
+                       [--only c2,...] [--extras] [--sweep] [--report PATH]
 """
 
 from __future__ import annotations
@@ -671,6 +677,161 @@ def reference_table(torch, fh, device, sizes=(4, 8, 16, 32), batches=(65536,), d
             "rows": rows}
 
 
+HEADLINE_KERNEL = "expm_p4_dma_kernel<F32, true, 2, 1> (Frechet backward, P=4, buffer-to-LDS loads)"
+LINE_LIMIT = 8000  # bytes: the stdout line must sit wholly inside a driver's captured tail
+
+
+def full_report(args, results: dict, cold, table, latency, mix_rows) -> dict:
+    """Everything the run measured, keyed as the compact line's fields plus the detail (every
+    trial, every config's kernels, the reference table, the stream-mixing sweep)."""
+    head = results.get("c2")
+    full = {
+        "metric": METRIC,
+        "value": head["matrices_per_s_fwd_bwd"] if head else None,
+        "unit": "matrices/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "settle_s": args.settle,
+        "ms_per_step": head["ms_step"] if head else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded, BASELINE config 2 distribution)",
+        "config": {
+            "workload": "BASELINE config 2: fh.matrix_exp forward + autograd backward on [1048576,4,4] FP32, "
+            "x ~ N(0,0.25^2), grad ~ N(0,1)",
+            "global_batch": 1 << 20,
+            "n": 4,
+            "parallelism": "single GPU",
+        },
+    }
+    if head:
+        b = 1 << 20
+        bytes_bwd = b * 16 * 3 * 4
+        achieved = head["bwd_kernel"]["achieved_gbs"]
+        full["trials"] = len(head["ms_step_trials"])
+        full["trials_ms"] = head["ms_step_trials"]
+        full["roofline"] = {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": profiled_traffic("expm_p4_frechet_c2_f32"),
+            "traffic_source": "profiles/expm_p4_c2_hbm_traffic.md (FETCH_SIZE, WRITE_SIZE; copy-calibrated)",
+            "kernel": HEADLINE_KERNEL,
+            "algorithmic_bytes_per_launch": bytes_bwd,
+            "median_launch_ms": head["ms_bwd_kernel"],
+            "launch_trials_ms": head["ms_bwd_trials"],
+        }
+        full["step_roofline_frac"] = head["roofline_frac_step"]
+        if cold is not None:
+            full["cold_step"] = cold
+            full["cold_over_warm"] = cold["ms_step"] / head["ms_step"]
+            # Same algorithmic bytes, the step's time with no operand in the last-level cache.
+            full["cold_step_roofline_frac"] = head["roofline_frac_step"] * head["ms_step"] / cold["ms_step"]
+    if latency is not None:
+        full["small_batch_latency"] = latency
+        full["reference_table"] = table
+    if mix_rows is not None:
+        full["mix_sweep"] = mix_rows
+    full["configs"] = results
+    return full
+
+
+def _r(v, digits: int = 4):
+    """v rounded to `digits` significant digits (None and non-floats pass through)."""
+    if isinstance(v, float) and v == v and v not in (float("inf"), float("-inf")) and v != 0.0:
+        return float(f"{v:.{digits}g}")
+    return v
+
+
+def compact_line(full: dict) -> dict:
+    """The stdout JSON line: the driver's required keys, the roofline and CPU baseline, and one
+    short summary per config (step / forward / backward microseconds, roofline fraction) and per
+    parity gate (counts only).  Bounded well under LINE_LIMIT bytes whatever the configs hold."""
+    keys = ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better", "scaling",
+            "vs_baseline", "dtype", "data", "config")
+    line = {k: full.get(k) for k in keys}
+    line["value"], line["ms_per_step"] = _r(line["value"], 6), _r(line["ms_per_step"], 6)
+    line["timing"] = (f"median of {full.get('trials', 0)} consecutive trials of the K timed steps (HIP events, "
+                      f"one sync each side); each config first runs {full.get('settle_s')} s of untimed steps, "
+                      f"then the W warmup steps")
+    if "trials_ms" in full:
+        line["trials_ms"] = [_r(t) for t in full["trials_ms"]]
+    if "roofline" in full:
+        rf = full["roofline"]
+        line["roofline"] = {k: _r(rf[k]) for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")}
+        line["roofline"]["traffic"] = rf["traffic"]  # bytes per launch, an integer
+        line["roofline"]["kernel"] = rf["kernel"]
+        line["roofline"]["algorithmic_bytes_per_launch"] = rf["algorithmic_bytes_per_launch"]
+        line["roofline"]["median_launch_ms"] = _r(rf["median_launch_ms"])
+        line["step_roofline_frac"] = _r(full.get("step_roofline_frac"), 3)
+    if "cold_step" in full:
+        line["cold_step"] = {"ms": _r(full["cold_step"]["ms_step"]), "sets": full["cold_step"]["sets"],
+                             "step_roofline_frac": _r(full["cold_step_roofline_frac"], 3)}
+    if "cpu_baseline" in full:
+        cb = full["cpu_baseline"]
+        line["cpu_baseline"] = {"value": _r(cb["value"]), "unit": cb["unit"], "cores": cb["cores"],
+                                "kind": cb["kind"], "sample": cb["sample"][:400],
+                                "cpu_model": (cb.get("cpu_model") or "")[:80]}
+    if "cpu_oracle_port" in full:
+        line["cpu_oracle_port"] = {"value": _r(full["cpu_oracle_port"]["value"]), "cores": 1, "kind": "port"}
+    summary = {}
+    for name, res in (full.get("configs") or {}).items():
+        if "matrices_per_s_fwd_bwd" in res:
+            summary[name] = {"us": [_r(res["ms_step"] * 1e3), _r(res["ms_fwd_kernel"] * 1e3),
+                                    _r(res["ms_bwd_kernel"] * 1e3)],
+                             "frac": _r(res["roofline_frac_step"], 3), "bound": res["bound"],
+                             "rate": _r(res["matrices_per_s_fwd_bwd"], 3)}
+        elif "tokens_per_s_fwd_bwd" in res:
+            summary[name] = {"us": [_r(res["ms_step"] * 1e3), _r(res["ms_fwd_kernel"] * 1e3),
+                                    _r(res["ms_bwd_kernel"] * 1e3)],
+                             "frac": _r(res["roofline_frac_step"], 3), "bound": "hbm",
+                             "rate": _r(res["tokens_per_s_fwd_bwd"], 3),
+                             "composed_us": _r(res["composed_ms_step"] * 1e3)}
+    if summary:
+        line["configs"] = summary
+        line["configs_fields"] = "us = [step, forward kernel, backward kernel]; frac = step roofline fraction"
+    if "parity" in full:
+        par = full["parity"]
+        comp = {}
+        for name, rep in par["configs"].items():
+            if "forward" in rep:
+                comp[name] = {d: [r["s_mismatches"], r["bitwise_mismatches_vs_oracle"], r["strict_failures_kernel"],
+                                  r["strict_failures_oracle"], _r(r["max_excess_over_reference"], 3)]
+                              for d, r in rep.items()}
+            else:
+                comp[name] = [rep.get(k) for k in ("exp_bitwise_mismatches", "dh_bitwise_mismatches",
+                                                    "y_bound_violations", "dx_bound_violations", "de_bound_violations")]
+        line["parity"] = {
+            "pass": par["pass"],
+            "failures": {k: str(v)[:200] for k, v in list(par["failures"].items())[:8]},
+            "configs": comp,
+            "fields": "matrices: [s mismatches, bitwise mismatches vs oracle, strict failures kernel, strict "
+                      "failures oracle, max excess over the oracle's error]; mixing: [exp(h) bit mismatches, dh "
+                      "bit mismatches, y / dx / dE bound violations]",
+        }
+    if full.get("small_batch_latency"):
+        lat = full["small_batch_latency"]
+        line["small_batch_latency_us"] = {k: _r(lat[k], 3) for k in (
+            "fh_forward", "fh_forward_backward", "trivial_op_forward_backward", "native_forward_backward")}
+    if full.get("reference_table"):
+        rows = full["reference_table"]["rows"]
+        line["reference_table_us"] = [[r["n"], r["batch"], r["dtype"], r["mode"][:3] if r["mode"] == "forward"
+                                       else "f+b", _r(r["median_us"], 3), r.get("reference_a100_us")]
+                                      for r in rows][:64]
+    size = len(json.dumps(line))
+    if size > LINE_LIMIT:  # never let the line outgrow the limit: drop the optional summaries
+        for k in ("reference_table_us", "configs", "small_batch_latency_us", "trials_ms"):
+            line.pop(k, None)
+            if len(json.dumps(line)) <= LINE_LIMIT:
+                break
+    return line
+
+
 def main() -> int:
     global SETTLE_S
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -687,6 +848,8 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true",
                     help="reference table over B in {1,128,1024,65536} x {f32,f16,bf16} (the reference's sweep), "
                     "and fused vs composed stream mixing over n and C")
+    ap.add_argument("--report", default="gpurun_out/bench_report.json",
+                    help="file (relative to the repo root) for the full JSON report; '' to skip")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one device copy of exactly 64 MiB (profiler counter calibration)")
     args = ap.parse_args()
@@ -753,63 +916,24 @@ def main() -> int:
         log("[bench] small-batch latency ...")
         latency = small_batch_latency(torch, fh, device)
         log(f"[bench] small-batch latency: {json.dumps(latency)}")
-    line = {
-        "metric": METRIC,
-        "value": head["matrices_per_s_fwd_bwd"] if head else None,
-        "unit": "matrices/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "settle_s": args.settle,
-        "ms_per_step": head["ms_step"] if head else None,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (seeded, BASELINE config 2 distribution)",
-        "config": {
-            "workload": "BASELINE config 2: fh.matrix_exp forward + autograd backward on [1048576,4,4] FP32, "
-            "x ~ N(0,0.25^2), grad ~ N(0,1)",
-            "global_batch": 1 << 20,
-            "n": 4,
-            "parallelism": "single GPU",
-        },
-    }
-    if head:
-        b = 1 << 20
-        bytes_bwd = b * 16 * 3 * 4
-        achieved = head["bwd_kernel"]["achieved_gbs"]
-        line["trials"] = len(head["ms_step_trials"])
-        line["trials_ms"] = head["ms_step_trials"]
-        line["roofline"] = {
-            "bound": "hbm",
-            "achieved": achieved,
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS,
-            "traffic": profiled_traffic("expm_p4_frechet_c2_f32"),
-            "traffic_source": "profiles/expm_p4_c2_hbm_traffic.md (FETCH_SIZE, WRITE_SIZE; copy-calibrated)",
-            "kernel": "expm_p4_dma_kernel<F32, true, 2, 1> (Frechet backward, P=4, buffer-to-LDS loads)",
-            "algorithmic_bytes_per_launch": bytes_bwd,
-            "median_launch_ms": head["ms_bwd_kernel"],
-            "launch_trials_ms": head["ms_bwd_trials"],
-        }
-        line["step_roofline_frac"] = head["roofline_frac_step"]
-        if cold is not None:
-            line["cold_step"] = cold
-            line["cold_over_warm"] = cold["ms_step"] / head["ms_step"]
+    full = full_report(args, results, cold, table, latency, mix_rows)
     if not args.skip_cpu:
         log("[bench] cpu leg ...")
         leg = cpu_leg(torch, kept, mix_kept)
-        line["cpu_baseline"] = leg["cpu_baseline"]
-        line["cpu_oracle_port"] = leg["cpu_oracle_port"]
-        line["parity"] = leg["parity"]
-    if latency is not None:
-        line["small_batch_latency"] = latency
-        line["reference_table"] = table
-    if mix_rows is not None:
-        line["mix_sweep"] = mix_rows
-    line["configs"] = results
+        full.update(leg)
+    line = compact_line(full)
+    # The whole report (every trial, every config's kernels, full parity reports, the reference
+    # table) goes to a file and to stderr; stdout carries one compact line.
+    text = json.dumps(full)
+    log("[bench] full report: " + text)
+    if args.report:
+        report = Path(args.report) if Path(args.report).is_absolute() else ROOT / args.report
+        try:
+            report.parent.mkdir(parents=True, exist_ok=True)
+            report.write_text(text + "\n")
+            line["report"] = args.report
+        except OSError as exc:
+            log(f"[bench] could not write {args.report}: {exc}")
     print(json.dumps(line), flush=True)
     return 0
 

@@ -121,12 +121,26 @@ int launch(const void* input, const int64_t input_strides[3], int input_neg, con
 // each token's rows spanning less than 2 GiB.
 // Rows of a streamed operand ([B, n, C], unit column stride): 16-byte aligned,
 // strides and C whole 16-byte vectors, each token's rows spanning < 2 GiB.
-bool stream_rows_ok(const void* p, const int64_t* st, int n, int64_t cols, int dtype) {
-  constexpr int64_t kSpan = int64_t{1} << 31;  // bytes one token's rows may span (32-bit buffer offsets)
-  const int64_t es = element_size(dtype);
-  const int64_t v = 16 / es;
+constexpr int64_t kSpan = int64_t{1} << 31;  // bytes one token's rows may span (32-bit buffer offsets)
+
+// Layout the streaming kernels read in place: contiguous, 16-byte aligned rows
+// whose length and strides are whole 16-byte vectors.
+bool stream_rows_ok(const void* p, const int64_t* st, int64_t cols, int dtype) {
+  const int64_t v = 16 / element_size(dtype);
   return st != nullptr && aligned(p, 16) && st[2] == 1 && st[0] >= 0 && st[1] >= 0 && st[0] % v == 0 &&
-         st[1] % v == 0 && cols % v == 0 && st[1] < kSpan && cols < kSpan && ((n - 1) * st[1] + cols) * es < kSpan;
+         st[1] % v == 0 && cols % v == 0;
+}
+
+// One token's n rows, read through row stride st[1], and the contiguous output
+// token (n * cols elements) each span < 2 GiB: the kernels address a token
+// through one buffer resource with 32-bit offsets.
+bool stream_span_ok(const int64_t* st, int n, int64_t cols, int dtype) {
+  const int64_t es = element_size(dtype);
+  return st[1] < kSpan && cols < kSpan && ((n - 1) * st[1] + cols) * es < kSpan && n * cols * es < kSpan;
+}
+
+std::string span_message(const char* op) {
+  return std::string(op) + ": one token's rows of X, dY and of the output must each span less than 2 GiB";
 }
 
 bool known_dtype(int dtype) { return dtype == FH_DTYPE_F32 || dtype == FH_DTYPE_BF16 || dtype == FH_DTYPE_F16; }
@@ -145,9 +159,11 @@ int validate_hc(const void* h, const int64_t* hs, const void* x, const int64_t* 
   if (batch == 0) return FH_OK;
   if (h == nullptr || hs == nullptr || x == nullptr || xs == nullptr || out == nullptr)
     return fail(FH_ERR_INVALID_ARGUMENT, "hc_mix: null pointer");
-  if (!stream_rows_ok(x, xs, n, cols, dtype) || (g != nullptr && !stream_rows_ok(g, gs, n, cols, dtype)) ||
+  if (!stream_rows_ok(x, xs, cols, dtype) || (g != nullptr && !stream_rows_ok(g, gs, cols, dtype)) ||
       !aligned(out, 16))
     return fail(FH_ERR_INVALID_ARGUMENT, rows_message("hc_mix", dtype));
+  if (!stream_span_ok(xs, n, cols, dtype) || (g != nullptr && !stream_span_ok(gs, n, cols, dtype)))
+    return fail(FH_ERR_INVALID_ARGUMENT, span_message("hc_mix"));
   return FH_OK;
 }
 
@@ -162,9 +178,11 @@ int validate_apply(const float* e, const void* x, const int64_t* xs, const void*
   if (e == nullptr || x == nullptr || xs == nullptr || out == nullptr)
     return fail(FH_ERR_INVALID_ARGUMENT, "hc_apply: null pointer");
   if (!aligned(e, 4)) return fail(FH_ERR_INVALID_ARGUMENT, "hc_apply: E must be 4-byte aligned float32");
-  if (!stream_rows_ok(x, xs, n, cols, dtype) || (g != nullptr && !stream_rows_ok(g, gs, n, cols, dtype)) ||
+  if (!stream_rows_ok(x, xs, cols, dtype) || (g != nullptr && !stream_rows_ok(g, gs, cols, dtype)) ||
       !aligned(out, 16))
     return fail(FH_ERR_INVALID_ARGUMENT, rows_message("hc_apply", dtype));
+  if (!stream_span_ok(xs, n, cols, dtype) || (g != nullptr && !stream_span_ok(gs, n, cols, dtype)))
+    return fail(FH_ERR_INVALID_ARGUMENT, span_message("hc_apply"));
   return FH_OK;
 }
 

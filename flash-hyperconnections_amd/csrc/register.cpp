@@ -19,8 +19,11 @@
 #include <Python.h>
 
 #include <ATen/ATen.h>
+#include <ATen/PythonTorchFunctionTLS.h>
 #include <ATen/core/dispatch/Dispatcher.h>
 #include <torch/autograd.h>
+#include <torch/csrc/Exceptions.h>
+#include <torch/csrc/autograd/python_variable.h>
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 #include <torch/library.h>
@@ -138,13 +141,18 @@ void check_mix(const at::Tensor& h, const at::Tensor& x) {
               "mix_streams: expected x [B, n, C] of h's dtype and device, C >= 1");
 }
 
-// Rows contiguous, 16-byte aligned, strides and C in whole 16-byte vectors:
-// what the kernel reads in place; anything else is copied once.
+// Rows contiguous, 16-byte aligned, strides and C in whole 16-byte vectors,
+// one token's rows spanning < 2 GiB (the kernels' 32-bit buffer offsets):
+// what the kernel reads in place; anything else is copied once (the copy's
+// token spans n * C elements, which the Python routing keeps < 2 GiB).
 at::Tensor streamable(const at::Tensor& x) {
-  const int64_t v = 16 / static_cast<int64_t>(x.element_size());
+  const int64_t es = static_cast<int64_t>(x.element_size());
+  const int64_t v = 16 / es;
+  constexpr int64_t kSpan = int64_t{1} << 31;
   const bool ok = !x.is_neg() && x.stride(2) == 1 && x.stride(1) % v == 0 && x.stride(0) % v == 0 &&
                   x.stride(0) >= 0 && x.stride(1) >= 0 && x.size(2) % v == 0 &&
-                  reinterpret_cast<uintptr_t>(x.const_data_ptr()) % 16 == 0;
+                  reinterpret_cast<uintptr_t>(x.const_data_ptr()) % 16 == 0 && x.stride(1) < kSpan &&
+                  ((x.size(1) - 1) * x.stride(1) + x.size(2)) * es < kSpan;
   if (ok) return x;
   at::Tensor c = x.resolve_neg().contiguous();
   if (x.size(2) % v == 0 && reinterpret_cast<uintptr_t>(c.const_data_ptr()) % 16 == 0) return c;
@@ -307,16 +315,61 @@ at::Tensor frechet_differentiable(const at::Tensor& input, const at::Tensor& dir
   return top_right(matrix_exp_op().call(frechet_block(input, direction)), input.size(-1), input.scalar_type());
 }
 
-// Gradient of exp at A against G, L(A^T, G) (reference :65-74).  Forward-mode
-// tangents take the native block exponential, as the reference does; a
-// backward that builds a graph (create_graph=True) takes the differentiable
-// block through this operator; otherwise the Frechet kernel.  Tensors with a
-// __torch_dispatch__ (fake, functional, user subclasses) take the same
-// branches and reach their handlers through the dispatcher; Python-level
-// __torch_function__ overrides are not visible here (the reference checks
-// them in its Python backward, but the Python entry point already sends such
-// subclasses to the native exponential).
+// Whether a tensor's Python object (if Python ever saw it) is of a type other
+// than torch.Tensor, i.e. may override __torch_function__.  Decided without the
+// interpreter: the object stays alive while the tensor does, and its type
+// pointer is fixed.
+bool python_type_may_override(const at::Tensor& t) {
+  PyObject* obj = t.unsafeGetTensorImpl()->pyobj_slot()->load_pyobj();
+  return obj != nullptr && Py_TYPE(obj) != reinterpret_cast<PyTypeObject*>(THPVariableClass);
+}
+
+// The reference's first backward branch (ops/matrix_exp/__init__.py:67-73):
+// when has_torch_function((input, grad_output)) holds -- a __torch_function__
+// mode is active (the autograd engine carries the caller's mode stack into the
+// backward) or an argument's Python type overrides __torch_function__ -- the
+// gradient is the native block exponential computed in Python, so that
+// subclasses see (and wrap) every call as they do in the reference.  The
+// check and that computation are the Python module's
+// (_torch_function_backward), called under the GIL only when the mode stack
+// or an argument's type can make the answer yes; otherwise returns an
+// undefined tensor at the cost of three loads.
+at::Tensor torch_function_gradient(const at::Tensor& input, const at::Tensor& grad) {
+  if (!at::impl::torch_function_mode_enabled() && !python_type_may_override(input) &&
+      !python_type_may_override(grad))
+    return {};
+  pybind11::gil_scoped_acquire gil;
+  at::Tensor out;
+  PyObject* module = PyImport_ImportModule("flash_hypercons.ops.matrix_exp");
+  PyObject* py_input = module ? THPVariable_Wrap(input) : nullptr;
+  PyObject* py_grad = py_input ? THPVariable_Wrap(grad) : nullptr;
+  PyObject* result =
+      py_grad ? PyObject_CallMethod(module, "_torch_function_backward", "OO", py_input, py_grad) : nullptr;
+  if (result != nullptr && result != Py_None) {
+    if (THPVariable_Check(result)) out = THPVariable_Unpack(result);
+    else PyErr_SetString(PyExc_TypeError, "_torch_function_backward must return a Tensor or None");
+  }
+  Py_XDECREF(result);
+  Py_XDECREF(py_grad);
+  Py_XDECREF(py_input);
+  Py_XDECREF(module);
+  if (PyErr_Occurred()) {
+    python_error err;  // holds the Python exception; the engine re-raises it in the caller
+    err.persist();
+    throw std::move(err);
+  }
+  return out;
+}
+
+// Gradient of exp at A against G, L(A^T, G) (reference :65-74).  The
+// __torch_function__ branch first (above); forward-mode tangents take the
+// native block exponential, as the reference does; a backward that builds a
+// graph (create_graph=True) takes the differentiable block through this
+// operator; otherwise the Frechet kernel.  Tensors with a __torch_dispatch__
+// (fake, functional, user subclasses) take the same branches and reach their
+// handlers through the dispatcher.
 at::Tensor exp_gradient(const at::Tensor& input, const at::Tensor& grad) {
+  if (at::Tensor via_python = torch_function_gradient(input, grad); via_python.defined()) return via_python;
   const at::Tensor a = input.mT();
   if (input._fw_grad(0).defined() || grad._fw_grad(0).defined()) return frechet_reference(a, grad);
   if (at::GradMode::is_enabled()) {

@@ -51,8 +51,18 @@ def _streamed(h: torch.Tensor, x: torch.Tensor) -> bool:
         and x.dtype == h.dtype
         and torch.autograd.forward_ad.unpack_dual(h).tangent is None
         and torch.autograd.forward_ad.unpack_dual(x).tangent is None
+        and _token_span(x) < 2**31
         and _device_supported(h.device.index)
     )
+
+
+def _token_span(x: torch.Tensor) -> int:
+    """Bytes of one token's n contiguous rows, C rounded up to whole 16-byte vectors: the span the
+    streaming kernels address with 32-bit offsets (inputs read in place span no more, or are copied
+    to this layout first)."""
+    es = x.element_size()
+    v = 16 // es
+    return x.shape[1] * (-(-x.shape[2] // v) * v) * es
 
 
 @torch.library.register_fake("flash_hypercons::_hc_mix")

@@ -135,6 +135,16 @@ def _backward(ctx, grad_output):
 
 
 
+def _torch_function_backward(input: torch.Tensor, grad_output: torch.Tensor):
+    """Reference :67-73, the backward's first branch, for the C++ autograd kernel of
+    ``_matrix_exp``: with a ``__torch_function__`` mode active or an argument whose type
+    overrides ``__torch_function__``, the gradient is the native block exponential computed
+    here (so subclasses see and wrap every call); otherwise None, and the kernel goes on."""
+    if has_torch_function((input, grad_output)):
+        return _frechet_reference(input.mT, grad_output)
+    return None
+
+
 def _tangent(input: torch.Tensor, tangent: torch.Tensor) -> torch.Tensor:
     """L(input, tangent), the forward-mode derivative of exp at input along tangent.
 

@@ -102,7 +102,9 @@ FH_API int fh_expm_params(const void* input, const int64_t input_strides[3], int
  * x [batch, n, cols], 2 <= n <= 4 streams; y is a contiguous [batch, n, cols]
  * array of the same dtype.  x's rows must be contiguous and 16-byte aligned,
  * with cols and x's strides multiples of 16 bytes' worth of elements (4 in
- * float32, 8 in float16/bfloat16) and each token's rows spanning < 2 GiB.
+ * float32, 8 in float16/bfloat16); each token's rows of x (and of grad) and
+ * its n * cols output elements must each span < 2 GiB (FH_ERR_INVALID_ARGUMENT
+ * with a span message otherwise).
  * exp(h[b]) is the same as fh_matrix_exp's (bit for bit) and never goes
  * to memory; e_out (float32 [batch, n, n], may be NULL) receives a copy.
  * No counterpart in the reference: its matrix_exp (flash_hypercons/ops/

@@ -33,7 +33,7 @@ AUTO = 0
 
 # Per-matrix sanity caps on the excess over the reference arithmetic (see direction_parity): far
 # above the scatter two FP32 summation orders show on the same matrix, far below any real mistake.
-EXCESS_LIMIT_F32 = 4.0  # ratio
+EXCESS_LIMIT_F32 = 2.0  # ratio (largest measured on every matrix of configs 2-5: 1.65)
 EXCESS_LIMIT_LOW = 2.0  # output ulps
 MEAN_ERROR_LIMIT = 1.05  # FP32 mean relative Frobenius error, kernel over restatement
 

@@ -12,6 +12,8 @@ register.cpp:10-24), checked against FP64 references and closed forms:
   transforms compile to native graphs;
 * autocast leaves the operator's dtype alone, Parameters are routed.
 
+The backward's __torch_function__ branch (a subclass gradient, or a mode active during the
+backward, sends it to the native block exponential) is pinned as the reference has it.
 Two deliberate differences from the reference are pinned here as well: an
 input carrying a forward-mode tangent gets its tangent from the Frechet kernel
 (row f1), and a backward that builds a graph differentiates this operator's own
@@ -115,6 +117,80 @@ def test_forward_mode_tangent_is_the_frechet_kernel(n, dtype, grad_mode):
         assert torch.equal(tangent, torch.ops.flash_hypercons._frechet(a, h))
         check_north_star(primal, reference(a))
         check_north_star(tangent, reference(a, h), backward=True)
+
+
+class _LoggingTensor(torch.Tensor):
+    """A __torch_function__ subclass that records the functions called on it."""
+
+    calls = []
+
+    @classmethod
+    def __torch_function__(cls, func, types, args=(), kwargs=None):
+        cls.calls.append(getattr(func, "__name__", str(func)))
+        return super().__torch_function__(func, types, args, kwargs or {})
+
+
+@pytest.mark.parametrize("n", [4, 9])
+def test_backward_with_a_torch_function_subclass_gradient(n):
+    """Reference :67-73: when the upstream gradient's type overrides __torch_function__, the
+    backward is the native block exponential computed through that type -- its result is the
+    subclass, its calls reach the subclass's handler, no Frechet kernel runs.  A plain gradient
+    on the same graph takes the kernel."""
+    a = (torch.randn(3, n, n, device="cuda") * 0.3).requires_grad_()
+    g_plain = torch.randn(3, n, n, device="cuda")
+    g = g_plain.as_subclass(_LoggingTensor)
+    _LoggingTensor.calls.clear()
+    y = fh.matrix_exp(a)
+    (grad,), names = profiled(lambda: torch.autograd.grad(y, a, g))
+    assert type(grad) is _LoggingTensor
+    assert FRECHET not in names and NATIVE in names
+    assert _LoggingTensor.calls, "the subclass saw no call"
+    check_error(grad.as_subclass(torch.Tensor), reference(a.detach().mT, g_plain), backward=True)
+    y = fh.matrix_exp(a)
+    (grad,), names = profiled(lambda: torch.autograd.grad(y, a, g_plain))
+    assert type(grad) is torch.Tensor and FRECHET in names and NATIVE not in names
+
+
+def test_backward_under_a_torch_function_mode():
+    """Reference :67-73 as well: has_torch_function is true while a __torch_function__ mode is
+    active, and the autograd engine carries the caller's modes into the backward, so a backward
+    run inside use_backend() (or any other such mode) is the native block exponential; the same
+    backward run outside the scope takes the Frechet kernel.  Parameters (whose type disables
+    __torch_function__) take the kernel."""
+    a = (torch.randn(3, 4, 4, device="cuda") * 0.3).requires_grad_()
+    g = torch.randn(3, 4, 4, device="cuda")
+    with fh.use_backend():
+        y = torch.linalg.matrix_exp(a)
+        (inside,), names = profiled(lambda: torch.autograd.grad(y, a, g))
+    assert FRECHET not in names and NATIVE in names
+    check_error(inside, reference(a.detach().mT, g), backward=True)
+    with fh.use_backend():
+        y = torch.linalg.matrix_exp(a)
+    (outside,), names = profiled(lambda: torch.autograd.grad(y, a, g))
+    assert FRECHET in names and NATIVE not in names
+    torch.testing.assert_close(inside, outside, rtol=1e-5, atol=1e-6)
+    p = torch.nn.Parameter(a.detach().clone())
+    (grad,), names = profiled(lambda: torch.autograd.grad(fh.matrix_exp(p), p, g))
+    assert FRECHET in names and type(grad) is torch.Tensor
+    assert torch.equal(grad, outside)
+
+
+def test_backward_python_errors_reach_the_caller():
+    """An exception raised by a subclass's handler inside the backward's native branch comes back
+    to the caller as that exception."""
+
+    class Failing(torch.Tensor):
+        @classmethod
+        def __torch_function__(cls, func, types, args=(), kwargs=None):
+            if getattr(func, "__name__", "") == "cat":
+                raise KeyError("from the subclass")
+            return super().__torch_function__(func, types, args, kwargs or {})
+
+    a = (torch.randn(2, 4, 4, device="cuda") * 0.3).requires_grad_()
+    g = torch.randn(2, 4, 4, device="cuda").as_subclass(Failing)
+    y = fh.matrix_exp(a)
+    with pytest.raises(KeyError, match="from the subclass"):
+        torch.autograd.grad(y, a, g)
 
 
 @pytest.mark.parametrize("layout", ["transposed", "expanded", "float64"])

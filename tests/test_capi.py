@@ -89,11 +89,19 @@ def test_hc_mix_validation_without_gpu():
         (xs, fake, 62),
         (xs, fake + 4, 64),
         ((ctypes.c_int64 * 3)(4 * 64, -64, 1), fake, 64),
-        ((ctypes.c_int64 * 3)(0, 1 << 29, 1), fake, 64),  # one token spans more than 2 GiB
     )
     for strides, ptr, cols in bad_rows:
         assert lib.fh_hc_mix(fake, hs, 0, ptr, strides, fake, None, 0, 2, 4, cols, None) == 1
         assert b"16-byte aligned rows" in lib.fh_last_error()
+    # Span: one token's input rows, or its contiguous output (n * C elements), at 2 GiB or more.
+    # Rows that overlap (row stride 0) keep the input's span small while the output's is not.
+    for strides, cols in (((ctypes.c_int64 * 3)(0, 1 << 29, 1), 64),
+                          ((ctypes.c_int64 * 3)(0, 0, 1), 1 << 27)):
+        assert lib.fh_hc_mix(fake, hs, 0, fake, strides, fake, None, 0, 2, 4, cols, None) == 1
+        assert b"span less than 2 GiB" in lib.fh_last_error()
+        assert lib.fh_hc_mix_backward(fake, hs, 0, fake, xs if cols == 64 else strides, fake, strides, fake, fake,
+                                      None, 0, 2, 4, cols, None) == 1
+        assert b"span less than 2 GiB" in lib.fh_last_error()
     # Backward: grad rows follow the same rule; grad and dh must be given.
     bad = (ctypes.c_int64 * 3)(4 * 64, 64, 2)
     assert lib.fh_hc_mix_backward(fake, hs, 0, fake, xs, fake, bad, fake, fake, None, 0, 2, 4, 64, None) == 1
@@ -126,10 +134,13 @@ def test_hc_apply_validation_without_gpu():
         ((ctypes.c_int64 * 3)(8 * 64, 68, 1), fake, 64),
         (xs, fake, 60),
         (xs, fake + 8, 64),
-        ((ctypes.c_int64 * 3)(0, 1 << 28, 1), fake, 64),  # one token spans more than 2 GiB
     ):
         assert lib.fh_hc_apply(fake, ptr, strides, fake, 1, 2, 8, cols, None) == 1
         assert b"16-byte aligned rows" in lib.fh_last_error() and b"multiples of 8" in lib.fh_last_error()
+    for strides, cols in (((ctypes.c_int64 * 3)(0, 1 << 28, 1), 64),  # input rows span more than 2 GiB
+                          ((ctypes.c_int64 * 3)(0, 0, 1), 1 << 27)):  # output token spans 2 GiB (8 x 2^27 BF16)
+        assert lib.fh_hc_apply(fake, fake, strides, fake, 1, 2, 8, cols, None) == 1
+        assert b"span less than 2 GiB" in lib.fh_last_error()
     bad = (ctypes.c_int64 * 3)(8 * 64, 64, 2)
     assert lib.fh_hc_apply_backward(fake, fake, xs, fake, bad, fake, fake, 0, 2, 8, 64, None) == 1
     assert b"16-byte aligned rows" in lib.fh_last_error()

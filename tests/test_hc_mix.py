@@ -211,6 +211,37 @@ def test_layouts_give_the_same_bits(hl, xl, dtype):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("n", [4, 8])
+def test_token_rows_spanning_2gib_are_copied_not_rejected(n):
+    """Token-major storage [n, B, C] viewed as [B, n, C]: a token's rows lie B*C elements apart.
+    With B large enough, one token's rows span more than the streaming kernels' 32-bit buffer
+    offsets reach; such operands (x and the upstream gradient) are copied to contiguous rows
+    first, so the results are the contiguous operands' bit for bit (n = 4: fused kernels; n = 8:
+    exp then the apply kernels)."""
+    dtype, c, tokens = torch.bfloat16, 4096, 16
+    b_total = 2**31 // ((n - 1) * c * 2) + 1
+    store_x = torch.empty(n, b_total, c, dtype=dtype, device="cuda")
+    store_g = torch.empty(n, b_total, c, dtype=dtype, device="cuda")
+    x = store_x.permute(1, 0, 2)[:tokens]
+    g = store_g.permute(1, 0, 2)[:tokens]
+    x.copy_(torch.randn(tokens, n, c, device="cuda").to(dtype))
+    g.copy_(torch.randn(tokens, n, c, device="cuda").to(dtype))
+    assert ((n - 1) * x.stride(1) + c) * x.element_size() >= 2**31
+    h = (torch.randn(tokens, n, n, device="cuda") * 0.5).to(dtype)
+    xc, gc = x.contiguous(), g.contiguous()
+    y = fh.mix_streams(h, x)
+    assert same_bits(y, fh.mix_streams(h, xc))
+    e64, x64 = torch.linalg.matrix_exp(h.double()), x.double()
+    assert bool(((y.double() - e64 @ x64).abs() <= 2.0**-7 * (e64.abs() @ x64.abs()) + 1e-30).all())
+    hr, xr = h.clone().requires_grad_(), x.detach().requires_grad_()
+    dh, dx = torch.autograd.grad(fh.mix_streams(hr, xr), (hr, xr), g)
+    hr2, xr2 = h.clone().requires_grad_(), xc.clone().requires_grad_()
+    dh_c, dx_c = torch.autograd.grad(fh.mix_streams(hr2, xr2), (hr2, xr2), gc)
+    assert same_bits(dh, dh_c) and same_bits(dx, dx_c)
+    del store_x, store_g, x, g
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=str)
 def test_tokens_do_not_depend_on_the_batch(dtype):
     # 40,000 tokens: more token blocks than the grid holds, so the grid-stride loop is used.

@@ -353,6 +353,14 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
 #pragma unroll
         for (int c = 0; c < 4; ++c) cur.d.v[4 * r + c] = h.v[4 * c + r];
       cur.u = read_token(gtile, slot);
+      // The debug copy of dE goes out now, so that cur.u is not kept live
+      // across the Frechet polynomial (it would spill at the 256-VGPR cap).
+      if (a.aux && lane < kTokens) {
+#pragma unroll
+        for (int r = 0; r < N; ++r)
+#pragma unroll
+          for (int k = 0; k < N; ++k) a.aux[b * N * N + r * N + k] = cur.u.v[4 * r + k];
+      }
     } else {
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
@@ -366,15 +374,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
 #pragma unroll
       for (int q = 0; q < 16; ++q) dh.v[q] = __builtin_nanf("");
     }
-    if (lane < kTokens && valid) {
-      store_elements<T>(a.dh, b, N, dh);
-      if (a.aux) {
-#pragma unroll
-        for (int r = 0; r < N; ++r)
-#pragma unroll
-          for (int k = 0; k < N; ++k) a.aux[b * N * N + r * N + k] = cur.u.v[4 * r + k];
-      }
-    }
+    if (lane < kTokens && valid) store_elements<T>(a.dh, b, N, dh);
     lds_order();
   }
 }

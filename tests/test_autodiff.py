@@ -152,27 +152,36 @@ def test_backward_with_a_torch_function_subclass_gradient(n):
 
 
 def test_backward_under_a_torch_function_mode():
-    """Reference :67-73 as well: has_torch_function is true while a __torch_function__ mode is
-    active, and the autograd engine carries the caller's modes into the backward, so a backward
-    run inside use_backend() (or any other such mode) is the native block exponential; the same
-    backward run outside the scope takes the Frechet kernel.  Parameters (whose type disables
+    """Reference :67-73 as well: has_torch_function is also true while a __torch_function__ mode
+    is active during the backward.  torch.autograd.grad and Tensor.backward dispatch through an
+    active mode, which is popped while its handler runs, so a backward started inside
+    use_backend() still finds no mode and takes the Frechet kernel (in the reference too).  A
+    mode that is active when the engine itself runs (entered below the Python entry points) sends
+    the backward to the native block exponential.  Parameters (whose type disables
     __torch_function__) take the kernel."""
+    from torch.autograd.graph import _engine_run_backward
+    from torch.overrides import TorchFunctionMode
+
+    class Passthrough(TorchFunctionMode):
+        def __torch_function__(self, func, types, args=(), kwargs=None):
+            return func(*args, **(kwargs or {}))
+
     a = (torch.randn(3, 4, 4, device="cuda") * 0.3).requires_grad_()
     g = torch.randn(3, 4, 4, device="cuda")
     with fh.use_backend():
         y = torch.linalg.matrix_exp(a)
-        (inside,), names = profiled(lambda: torch.autograd.grad(y, a, g))
+        (scoped,), names = profiled(lambda: torch.autograd.grad(y, a, g))
+    assert FRECHET in names and NATIVE not in names
+    y = fh.matrix_exp(a)
+    with Passthrough():
+        (inside,), names = profiled(lambda: _engine_run_backward((y,), (g,), False, False, (a,), True, False))
     assert FRECHET not in names and NATIVE in names
     check_error(inside, reference(a.detach().mT, g), backward=True)
-    with fh.use_backend():
-        y = torch.linalg.matrix_exp(a)
-    (outside,), names = profiled(lambda: torch.autograd.grad(y, a, g))
-    assert FRECHET in names and NATIVE not in names
-    torch.testing.assert_close(inside, outside, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(inside, scoped, rtol=1e-5, atol=1e-6)
     p = torch.nn.Parameter(a.detach().clone())
     (grad,), names = profiled(lambda: torch.autograd.grad(fh.matrix_exp(p), p, g))
     assert FRECHET in names and type(grad) is torch.Tensor
-    assert torch.equal(grad, outside)
+    assert torch.equal(grad, scoped)
 
 
 def test_backward_python_errors_reach_the_caller():

@@ -1,4 +1,5 @@
-"""Generated code: no wide vector store has its data overwritten by the next instruction.
+"""Generated code: no wide vector store has its data overwritten by the next instruction, and
+the kernels on the measured paths spill no registers to scratch.
 
 A vector-memory store of more than 8 bytes reads its data registers after it
 issues.  The compiler separates such a store from a following write of those
@@ -67,9 +68,38 @@ def _assembly(source: str, out: Path) -> str:
     return out.read_text()
 
 
-def test_kernels_keep_store_data_until_read(tmp_path):
+@pytest.fixture(scope="module")
+def assembly(tmp_path_factory):
+    """gfx950 assembly of every kernel source, compiled once for this module's tests."""
+    out = tmp_path_factory.mktemp("asm")
     sources = [s for s in fh_build.KERNEL_SOURCES if s.endswith(".hip")]
     with ThreadPoolExecutor(max_workers=min(8, len(sources))) as pool:  # one hipcc process per source
-        asm = dict(zip(sources, pool.map(lambda s: _assembly(s, tmp_path / (s + ".s")), sources)))
-    found = [f"{src}: {hit}" for src, text in asm.items() for hit in overwritten_stores(text)]
+        return dict(zip(sources, pool.map(lambda s: _assembly(s, out / (s + ".s")), sources)))
+
+
+def test_kernels_keep_store_data_until_read(assembly):
+    found = [f"{src}: {hit}" for src, text in assembly.items() for hit in overwritten_stores(text)]
     assert not found, "\n".join(found[:5])
+
+
+KERNEL_SCRATCH = re.compile(r"\.amdhsa_kernel (\S+)\n(?:.*\n)*?\s*\.amdhsa_private_segment_fixed_size (\d+)")
+
+# Kernels on the measured paths: the P = 4 dense (buffer-to-LDS) and count-ordered kernels, the
+# P = 8 and tile kernels, and the stream-mixing kernels.  Register spills there would add scratch
+# traffic to the HBM-bound launches.
+NO_SCRATCH = ("expm_p4_dma_kernel", "expm_p4_sort_kernel", "expm_oct_kernel", "expm_oct16", "expm_tile_kernel",
+              "hc_mix_fwd_kernel", "hc_mix_bwd_kernel", "hc_wide_fwd_kernel", "hc_wide_bwd_kernel")
+
+
+def test_scanner_reads_scratch_sizes():
+    asm = ("\t.amdhsa_kernel _Zk1\n\t\t.amdhsa_group_segment_fixed_size 0\n\t\t.amdhsa_private_segment_fixed_size 64\n"
+           "\t.amdhsa_kernel _Zk2\n\t\t.amdhsa_private_segment_fixed_size 0\n")
+    assert KERNEL_SCRATCH.findall(asm) == [("_Zk1", "64"), ("_Zk2", "0")]
+
+
+def test_measured_kernels_use_no_scratch(assembly):
+    sizes = {name: int(size) for text in assembly.values() for name, size in KERNEL_SCRATCH.findall(text)}
+    hot = {name: size for name, size in sizes.items() if any(k in name for k in NO_SCRATCH)}
+    assert len(hot) > 60, sorted(hot)  # every instantiation of those kernels was found
+    spilling = {name: size for name, size in hot.items() if size}
+    assert not spilling, spilling

@@ -447,14 +447,13 @@ __global__ __launch_bounds__(64 * kOctWaves) __attribute__((amdgpu_waves_per_eu(
     } else {
       ac = lx;
     }
-    PR<Pair> ar, acol;
-    prowcols<Pair>(ac, t, lane, ar, acol);
-
     const int s = matrix_squarings<Pair>(ac, I);
     const bool bad = s < 0;
 
     // Scale by 2^-s (csrc/MatrixExpSmall.cuh:157-162) with the views' lazy
-    // negation folded into the same exact multiply.
+    // negation folded into the same exact multiply, before the rows and
+    // columns are formed: the LDS moves copy the scaled values as they are,
+    // so one multiply per C-layout entry serves all three layouts.
     const float scale = __builtin_ldexpf(1.f, bad ? 0 : -s);
     const float scale_x = scale * args.x.sign;
     const float scale_g = scale * args.g.sign;
@@ -463,15 +462,8 @@ __global__ __launch_bounds__(64 * kOctWaves) __attribute__((amdgpu_waves_per_eu(
       ac.d.v[r] *= scale_x;
       if constexpr (Pair) ac.u.v[r] *= scale_g;
     }
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      ar.d.v[r] *= scale_x;
-      acol.d.v[r] *= scale_x;
-      if constexpr (Pair) {
-        ar.u.v[r] *= scale_g;
-        acol.u.v[r] *= scale_g;
-      }
-    }
+    PR<Pair> ar, acol;
+    prowcols<Pair>(ac, t, lane, ar, acol);
 
     PQ<Pair> res = t18<Pair>(ar, acol, ac, diag, t, lane);
 

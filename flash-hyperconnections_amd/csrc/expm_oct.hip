@@ -473,7 +473,22 @@ __global__ __launch_bounds__(64 * kOctWaves) __attribute__((amdgpu_waves_per_eu(
     for (int it = 0; __builtin_amdgcn_ballot_w64(it < s) != 0; ++it) {
       PR<Pair> rr, rc;
       prowcols<Pair>(res, t, lane, rr, rc);
-      const PQ<Pair> sq = pmm<Pair>(rr, rc);
+      PQ<Pair> sq;
+      if constexpr (Pair) {
+        if (__builtin_amdgcn_ballot_w64(it + 1 < s) == 0) {
+          // The wavefront's last round: nothing reads its D block, so only
+          // the U sums run (as pmm forms them).
+          const Q u = chain(rr.d, rc.u);
+          const Q v = chain(rr.u, rc.d);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sq.u.v[r] = u.v[r] + v.v[r];
+          sq.d = res.d;
+        } else {
+          sq = pmm<Pair>(rr, rc);
+        }
+      } else {
+        sq = pmm<Pair>(rr, rc);
+      }
       const bool keep = it < s;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {

@@ -119,20 +119,26 @@ __device__ __forceinline__ Acc<P> mma(const Tm<P>& xt, const Tm<P>& y, Acc<P> ac
 
 // (D1, U1).(D2, U2) = (D1.D2, D1.U2 + U1.D2).  Step r feeds all three
 // products, so each operand register dies after its step and the D and U
-// accumulations alternate as two independent MFMA chains.
-template <int P, bool Pair>
+// accumulations alternate as two independent MFMA chains.  WantD = false
+// skips the D chain (a last squaring, whose D block nothing reads); the D
+// block is then left as x's.
+template <int P, bool Pair, bool WantD = true>
 __device__ __forceinline__ PTm<P, Pair> pmm(const PTm<P, Pair>& xt, const PTm<P, Pair>& y) {
   Acc<P> d = {}, u = {};
 #pragma unroll
   for (int r = 0; r < TileCfg<P>::R; ++r) {
-    d = TileCfg<P>::mfma(xt.d.v[r], y.d.v[r], d);
+    if constexpr (WantD) d = TileCfg<P>::mfma(xt.d.v[r], y.d.v[r], d);
     if constexpr (Pair) {
       u = TileCfg<P>::mfma(xt.d.v[r], y.u.v[r], u);
       u = TileCfg<P>::mfma(xt.u.v[r], y.d.v[r], u);
     }
   }
   PTm<P, Pair> out;
-  out.d = from_acc<P>(d);
+  if constexpr (WantD) {
+    out.d = from_acc<P>(d);
+  } else {
+    out.d = y.d;
+  }
   if constexpr (Pair) out.u = from_acc<P>(u);
   return out;
 }
@@ -511,7 +517,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kTileWaves<P
     const PTm<P, Pair> lhst = ptranspose<P, Pair>(padd<P, Pair>(combine<2, P, Pair>(a, a2, a3, a6, id), a9), buf, lane);
     const PTm<P, Pair> b2 = combine<1, P, Pair>(a, a2, a3, a6, id);
     PTm<P, Pair> res = padd<P, Pair>(b2, pmm<P, Pair>(lhst, a9));
-    for (int i = 0; i < s; ++i) res = pmm<P, Pair>(ptranspose<P, Pair>(res, buf, lane), res);
+    if constexpr (Pair) {
+      // The last squaring forms only the U block (the output).
+      for (int i = 1; i < s; ++i) res = pmm<P, Pair>(ptranspose<P, Pair>(res, buf, lane), res);
+      if (s > 0) res = pmm<P, Pair, false>(ptranspose<P, Pair>(res, buf, lane), res);
+    } else {
+      for (int i = 0; i < s; ++i) res = pmm<P, Pair>(ptranspose<P, Pair>(res, buf, lane), res);
+    }
 
     store_tile<T, P, Full>(args.out, b, n, lane_m, Pair ? res.u : res.d);
     if (lane == 0 && args.s_out) args.s_out[b] = s;

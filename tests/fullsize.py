@@ -196,7 +196,7 @@ def check(report: dict, n: int) -> list[str]:
     * no more matrices outside the strict north-star rule than the restatement has;
     * FP32: mean relative Frobenius error at most 1.05x the restatement's;
     * per matrix, the error above max(strict bound, restatement's error) stays under the sanity
-      cap (4x in FP32, 2 output ulps in FP16/BF16)."""
+      cap (2x in FP32, 2 output ulps in FP16/BF16)."""
     why = []
     if report["s_mismatches"]:
         why.append(f"{report['s_mismatches']} squaring counts differ")

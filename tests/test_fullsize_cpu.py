@@ -128,3 +128,36 @@ def test_normwise_reads_infinity_as_an_interval():
     r = error_ratio(act, ref, backward=False, normwise=True)
     assert abs(r[0].item() - 520 / 8192) < 1e-9
     assert abs(r[1].item() - 130520 / 8192) < 1e-9
+
+
+def test_sweep_overflow_rule_on_planted_results():
+    """The seeded sweep's rule for n >= 9 results the reference arithmetic overflows
+    (tests/test_parity_sweep.py::_mismatches), on a stand-in result made from the oracle: where
+    the oracle holds +-inf or NaN, a non-finite value of either kind or a finite one at the top of
+    the output range passes; an ordinary finite value fails, and so does a NaN where the oracle's
+    result is finite."""
+    from tests.test_parity_sweep import _mismatches
+
+    n, dtype = 10, torch.bfloat16
+    x = torch.eye(n, dtype=torch.float64).repeat(2, 1, 1) * torch.tensor([0.1, 100.0])[:, None, None]
+    x[1, 0, 1:] = 100.0  # exp(100) ~ 2.7e43: the exact exponential lies beyond the BF16/FP32 range
+    x = x.to(dtype)
+    want, want_s = oracle.torch_matrix_exp(x)
+    assert bool(torch.isfinite(want[0]).all()) and not bool(torch.isfinite(want[1]).all())
+    bad = (~torch.isfinite(want[1])).nonzero()[0].tolist()
+    top = torch.finfo(dtype).max
+
+    def planted(value):
+        out = want.clone()
+        out[1, bad[0], bad[1]] = value
+        return out
+
+    assert _mismatches(want, want_s, want, want_s, n, dtype) == []
+    other = float("nan") if not bool(want[1, bad[0], bad[1]].isnan()) else float("inf")
+    assert _mismatches(planted(other), want_s, want, want_s, n, dtype) == []
+    assert _mismatches(planted(0.99 * top), want_s, want, want_s, n, dtype) == []
+    assert _mismatches(planted(1.0), want_s, want, want_s, n, dtype)
+    assert _mismatches(planted(-0.5 * top), want_s, want, want_s, n, dtype)
+    out = want.clone()
+    out[0, 2, 3] = float("nan")
+    assert _mismatches(out, want_s, want, want_s, n, dtype)

@@ -391,26 +391,35 @@ __global__ __launch_bounds__(64 * kP4Waves) __attribute__((amdgpu_waves_per_eu(P
   if (group == full && static_cast<int64_t>(full) * 64 < args.batch) expm_group_elements<T, Pair>(args, group, lane);
 }
 
-// ---- 2-byte dtypes: pairs of groups ordered by squaring count ---------------
+// ---- 2-byte dtypes: batches of groups ordered by squaring count -------------
 //
 // A wavefront squares up to the largest count among its 64 matrices, so when
 // counts spread (inputs over several decades of norm) most of a group's
 // squaring rounds run for a few lanes.  For FP16/BF16 a wavefront's LDS holds
-// two groups' inputs per slot, still double-buffered: the kernel computes the
-// count of all 128 matrices, ranks them by (count, position) with a counting
-// sort over ballots, and runs two rounds of 64 in rank order, so the first
-// round squares only up to the median count.  Each matrix's result (already in
-// the output dtype, 32 bytes) replaces its own first input tuples in the slot,
-// from where both groups are stored coalesced.  Which lane computes a matrix
-// does not change what it computes, so results are the unsorted kernel's.
+// a batch of G groups' inputs per slot (SortSlot): the kernel computes the
+// count of all 64 G matrices, ranks them by (count, position) with a counting
+// sort over ballots, and runs G rounds of 64 in rank order, so the early
+// rounds square only up to low counts.  Each matrix's result (already in the
+// output dtype, 32 bytes) replaces its own first input tuples in the slot,
+// from where the batch's groups are stored coalesced.  Which lane computes a
+// matrix does not change what it computes, so results are the unsorted
+// kernel's.
 
+// Groups per batch and LDS slots per wavefront: two slots (the next batch
+// loads while this one computes) of two groups each.  Batches of four groups
+// in one slot (the same LDS) for the forward, which gives each wavefront one
+// batch, were bit-identical but no faster (config 3 forward 23.9 -> 24.3 us,
+// same process, alternating): half as many wavefronts and a longer ranking
+// loop outweigh the squaring rounds saved.
 template <typename T, bool Pair>
 struct SortSlot {
-  static_assert(sizeof(typename T::storage) == 2, "pairs of groups fit the LDS budget for 2-byte dtypes only");
+  static_assert(sizeof(typename T::storage) == 2, "batches of groups fit the LDS budget for 2-byte dtypes only");
+  static constexpr int G = 2;                            // groups per batch
+  static constexpr int kSlots = 2;                       // slots per wavefront
   static constexpr int C = Raw<T>::C;                    // tuples per matrix (2)
   static constexpr int kArea = C * kDenseRowBytes;       // one operand of one group
   static constexpr int kGroup = (Pair ? 2 : 1) * kArea;  // one group's inputs
-  static constexpr int kBytes = 2 * kGroup;              // the batch's two groups
+  static constexpr int kBytes = G * kGroup;              // the batch's groups
 };
 
 // Matrix m's tuples in an operand area of the slot (rows c * 1040, byte 16 m).
@@ -476,24 +485,38 @@ __device__ __forceinline__ void write_result_at(char* area, int m, const M4& v, 
 // write as 0x7FC0.
 constexpr int kNanFreeCount = 4;
 
-// Persistent kernel over batches of two full groups of a 2-byte dense batch
-// (n == 4): batch q is groups 2q and 2q + 1.
+// Units of a 2-byte dense batch (n == 4) for expm_p4_sort_kernel: the sorted
+// batches of G full groups, then one unit per group left over (the full
+// groups after the last batch and a partial last group), so that no
+// wavefront takes more than one of them.
+template <typename T, bool Pair>
+__host__ __device__ constexpr int64_t sort_units(int64_t batch) {
+  constexpr int G = SortSlot<T, Pair>::G;
+  const int64_t full = batch / 64;
+  return full / G + full % G + (full * 64 < batch ? 1 : 0);
+}
+
+// Kernel over batches of G full groups of a 2-byte dense batch (n == 4):
+// batch q is groups G q .. G q + G - 1; the units after the last batch are the
+// left-over groups, one per unit.
 template <typename T, bool Pair, int XL, int GL>
 __global__ __launch_bounds__(64 * kP4Waves) __attribute__((amdgpu_waves_per_eu(Pair ? 2 : 4, 8))) void expm_p4_sort_kernel(
     ExpmArgs args) {
   using Slot = SortSlot<T, Pair>;
+  constexpr int G = Slot::G;
   constexpr int C = Slot::C;
   constexpr int es = 2;
-  constexpr int kLoads = 2 * C * (Pair ? 2 : 1);  // load instructions per batch
+  constexpr int kLoads = G * C * (Pair ? 2 : 1);  // load instructions per batch
   constexpr int32_t kGroupBytes = 64 * 16 * es;
-  __shared__ __attribute__((aligned(16))) char tile_mem[kP4Waves][2][Slot::kBytes];
-  __shared__ uint8_t order_mem[kP4Waves][128];  // matrix (64 h + m) by rank
-  __shared__ int16_t count_mem[kP4Waves][128];  // squaring count by matrix
+  __shared__ __attribute__((aligned(16))) char tile_mem[kP4Waves][Slot::kSlots][Slot::kBytes];
+  __shared__ uint8_t order_mem[kP4Waves][G * 64];  // matrix (64 h + m) by rank
+  __shared__ int16_t count_mem[kP4Waves][G * 64];  // squaring count by matrix
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // Groups fit in 32 bits: the host takes this kernel only for operands below 2 GiB.
   const int32_t full = static_cast<int32_t>(args.batch / 64);
-  const int32_t batches = full / 2;
+  const int32_t batches = full / G;
+  const int32_t units = static_cast<int32_t>(sort_units<T, Pair>(args.batch));
   const int32_t stride = static_cast<int32_t>(gridDim.x) * kP4Waves;
   int32_t q = static_cast<int32_t>(blockIdx.x) * kP4Waves + wave;
   const U32x4 xs = rsrc_words(args.x.data);
@@ -504,9 +527,9 @@ __global__ __launch_bounds__(64 * kP4Waves) __attribute__((amdgpu_waves_per_eu(P
   auto issue = [&](int32_t b, char* slot) {
     const uint32_t a = lds_address(slot);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      load_group_to_lds<T>(xs, a + h * Slot::kGroup, (2 * b + h) * kGroupBytes, lane);
-      if constexpr (Pair) load_group_to_lds<T>(gs, a + h * Slot::kGroup + Slot::kArea, (2 * b + h) * kGroupBytes, lane);
+    for (int h = 0; h < G; ++h) {
+      load_group_to_lds<T>(xs, a + h * Slot::kGroup, (G * b + h) * kGroupBytes, lane);
+      if constexpr (Pair) load_group_to_lds<T>(gs, a + h * Slot::kGroup + Slot::kArea, (G * b + h) * kGroupBytes, lane);
     }
   };
   auto matrix_at = [&](const char* grp, int m) {
@@ -517,42 +540,51 @@ __global__ __launch_bounds__(64 * kP4Waves) __attribute__((amdgpu_waves_per_eu(P
   };
   int which = 0;
   if (q < batches) issue(q, tile_mem[wave][0]);
-  for (; q < batches; q += stride) {
+  for (bool first = true; q < batches; q += stride, first = false) {
     char* slot = tile_mem[wave][which];
-    if (q + stride < batches) {
-      issue(q + stride, tile_mem[wave][which ^ 1]);
-      wait_vm<kLoads>();
+    if constexpr (Slot::kSlots == 2) {
+      // The next batch's loads go to the other slot (its results were read
+      // out for the previous batch's stores); then wait for this batch's.
+      if (q + stride < batches) {
+        issue(q + stride, tile_mem[wave][which ^ 1]);
+        wait_vm<kLoads>();
+      } else {
+        wait_vm<0>();
+      }
     } else {
+      // One slot: a later batch of this wavefront loads once the previous
+      // batch's results have been read out of the slot for its stores.
+      if (!first) issue(q, slot);
       wait_vm<0>();
     }
     lds_order();
     // Squaring count of matrix `lane` of each group (-1: non-finite, squares as 0).
-    int sh[2];
+    int sh[G], kh[G], rh[G];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) sh[h] = lane_squarings<Pair>(matrix_at(slot + h * Slot::kGroup, lane));
-    // Rank by (count, matrix): counting sort, one ballot per count value and group.
-    const int k0 = sh[0] < 0 ? 0 : sh[0];
-    const int k1 = sh[1] < 0 ? 0 : sh[1];
-    int r0 = 0, r1 = 0, base = 0;
-    for (int v = 0; base < 128; ++v) {
-      const uint64_t b0 = __builtin_amdgcn_ballot_w64(k0 == v);
-      const uint64_t b1 = __builtin_amdgcn_ballot_w64(k1 == v);
-      if (k0 == v) r0 = base + lanes_below(b0);
-      base += __builtin_popcountll(b0);
-      if (k1 == v) r1 = base + lanes_below(b1);
-      base += __builtin_popcountll(b1);
+    for (int h = 0; h < G; ++h) {
+      sh[h] = lane_squarings<Pair>(matrix_at(slot + h * Slot::kGroup, lane));
+      kh[h] = sh[h] < 0 ? 0 : sh[h];
+      rh[h] = 0;
     }
-    order[r0] = static_cast<uint8_t>(lane);
-    order[r1] = static_cast<uint8_t>(64 + lane);
-    count[lane] = static_cast<int16_t>(sh[0]);  // at most ~130 for finite 2-byte inputs
-    count[64 + lane] = static_cast<int16_t>(sh[1]);
-    if (args.s_out) {
-      args.s_out[static_cast<int64_t>(2 * q) * 64 + lane] = sh[0];
-      args.s_out[static_cast<int64_t>(2 * q + 1) * 64 + lane] = sh[1];
+    // Rank by (count, matrix): counting sort, one ballot per count value and group.
+    int base = 0;
+    for (int v = 0; base < G * 64; ++v) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const uint64_t b = __builtin_amdgcn_ballot_w64(kh[h] == v);
+        if (kh[h] == v) rh[h] = base + lanes_below(b);
+        base += __builtin_popcountll(b);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      order[rh[h]] = static_cast<uint8_t>(64 * h + lane);
+      count[64 * h + lane] = static_cast<int16_t>(sh[h]);  // at most ~130 for finite 2-byte inputs
+      if (args.s_out) args.s_out[static_cast<int64_t>(G * q + h) * 64 + lane] = sh[h];
     }
     lds_order();
 #pragma unroll 1
-    for (int r = 0; r < 2; ++r) {
+    for (int r = 0; r < G; ++r) {
       const int id = order[64 * r + lane];
       const int s = count[id];
       char* grp = slot + (id >> 6) * Slot::kGroup;
@@ -570,23 +602,20 @@ __global__ __launch_bounds__(64 * kP4Waves) __attribute__((amdgpu_waves_per_eu(P
     lds_order();
     // Store instruction c of a group: lane l's tuple c, to tuple C l + c of the group's block.
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < G; ++h)
 #pragma unroll
       for (int c = 0; c < C; ++c) {
         const uint4 v = *reinterpret_cast<const uint4*>(slot + h * Slot::kGroup + c * kDenseRowBytes + 16 * lane);
         const U32x4 w = {v.x, v.y, v.z, v.w};
-        __builtin_amdgcn_raw_buffer_store_b128(w, out_rs, (2 * q + h) * kGroupBytes + 16 * (C * lane + c),
+        __builtin_amdgcn_raw_buffer_store_b128(w, out_rs, (G * q + h) * kGroupBytes + 16 * (C * lane + c),
                                                kStoreSOffset, kNontemporal);
       }
     lds_order();
-    which ^= 1;
+    if constexpr (Slot::kSlots == 2) which ^= 1;
   }
-  // The odd last full group and the partial last group, if any, belong to the
-  // wavefront whose walk reaches the end of the batches.
-  if (q == batches) {
-    if (full % 2) expm_group_elements<T, Pair>(args, full - 1, lane);
-    if (static_cast<int64_t>(full) * 64 < args.batch) expm_group_elements<T, Pair>(args, full, lane);
-  }
+  // The groups after the last batch (full ones, then the partial last group),
+  // one per unit.
+  for (; q < units; q += stride) expm_group_elements<T, Pair>(args, static_cast<int64_t>(batches) * G + (q - batches), lane);
 }
 
 // Every group of an element-class batch (n < 4 or strides no vector class
@@ -643,9 +672,8 @@ template <typename T, bool Pair, int XL, int GL>
 hipError_t launch_sort(const ExpmArgs& args, hipStream_t stream) {
   static const int64_t resident =
       resident_blocks(reinterpret_cast<const void*>(&expm_p4_sort_kernel<T, Pair, XL, GL>), 64 * kP4Waves);
-  // Batches of two full groups, plus the wavefront after them for the leftovers.
-  const int64_t units = args.batch / 128 + 1;
-  return launch_persistent(expm_p4_sort_kernel<T, Pair, XL, GL>, units, args, stream,
+  // Batches of G full groups, then one unit per left-over group.
+  return launch_persistent(expm_p4_sort_kernel<T, Pair, XL, GL>, sort_units<T, Pair>(args.batch), args, stream,
                            Pair ? resident : kForwardGridCap);
 }
 

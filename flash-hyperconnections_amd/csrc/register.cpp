@@ -326,10 +326,12 @@ bool python_type_may_override(const at::Tensor& t) {
 
 // The reference's first backward branch (ops/matrix_exp/__init__.py:67-73):
 // when has_torch_function((input, grad_output)) holds -- a __torch_function__
-// mode is active (the autograd engine carries the caller's mode stack into the
-// backward) or an argument's Python type overrides __torch_function__ -- the
-// gradient is the native block exponential computed in Python, so that
-// subclasses see (and wrap) every call as they do in the reference.  The
+// mode is active where the engine runs (the engine carries the caller's mode
+// stack into the backward; torch.autograd.grad and Tensor.backward themselves
+// dispatch through an active mode, which is popped while its handler runs) or
+// an argument's Python type overrides __torch_function__ -- the gradient is
+// the native block exponential computed in Python, so that subclasses see (and
+// wrap) every call as they do in the reference.  The
 // check and that computation are the Python module's
 // (_torch_function_backward), called under the GIL only when the mode stack
 // or an argument's type can make the answer yes; otherwise returns an

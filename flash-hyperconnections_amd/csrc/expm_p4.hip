@@ -706,10 +706,13 @@ hipError_t launch_vec_dense(const ExpmArgs& args, hipStream_t stream) {
 // offsets: every byte a group touches must lie below 2^31 with non-negative
 // strides; otherwise the element kernel (64-bit indexing) runs.
 bool vec_addressable(const Operand& op, int64_t batch, int es) {
-  if (op.sb < 0 || op.sr < 0 || op.sc < 0) return false;
+  constexpr int64_t kLimit = (int64_t{1} << 31) - 1024;
+  if (op.sb < 0 || op.sr < 0 || op.sc < 0 || op.sr > kLimit || op.sc > kLimit) return false;
   const int64_t groups = (batch + 63) / 64;
-  const int64_t last = (groups * 64 - 1) * op.sb + 3 * (op.sr + op.sc) + 4;
-  return last * es < (int64_t{1} << 31) - 1024;
+  int64_t last = 0;  // any overflow means far beyond the 32-bit offsets
+  if (__builtin_mul_overflow(groups * 64 - 1, op.sb, &last)) return false;
+  last += 3 * (op.sr + op.sc) + 4;
+  return last < kLimit / es;
 }
 
 template <typename T, bool Pair>
@@ -718,7 +721,7 @@ hipError_t launch_p4_t(const ExpmArgs& args, hipStream_t stream) {
   int xl = args.n == 4 ? args.x.vec : kVecNone;
   int gl = (Pair && args.n == 4) ? args.g.vec : kVecNone;
   const bool addressable = vec_addressable(args.x, args.batch, es) && (!Pair || vec_addressable(args.g, args.batch, es)) &&
-                           args.batch * 16 * es < (int64_t{1} << 31) - 1024;
+                           args.batch < ((int64_t{1} << 31) - 1024) / (16 * es);
   if (xl == kVecNone || (Pair && gl == kVecNone) || !addressable) {
     static const int64_t resident =
         resident_blocks(reinterpret_cast<const void*>(&expm_p4_elem_kernel<T, Pair>), 64 * kP4Waves);

@@ -15,7 +15,9 @@
  * contiguous [B, n, n] array in the input dtype.
  *
  * All pointers are device pointers of one HIP device, the current device of
- * the calling thread.  Launches are asynchronous on `stream`; nothing here
+ * the calling thread, and every view (pointer, strides, batch, n) must lie
+ * within an allocation on it: the library checks shapes, dtypes and its own
+ * addressing limits, not memory bounds.  Launches are asynchronous on `stream`; nothing here
  * synchronises, allocates device memory or keeps state across calls other
  * than the thread-local error message.
  *

@@ -18,8 +18,8 @@ directions (tests/fullsize.py):
 
 Each config prints its counts, so a run records them.
 
-The fused stream mixing's bench workload (``fh.mix_streams``, 16,384 tokens x
-4 streams x 4,096 columns, BF16) is checked over every token as well
+The fused stream mixing's bench workloads (``fh.mix_streams``, 16,384 tokens x
+4 and x 8 streams x 4,096 columns, BF16) are checked over every token as well
 (tests/mixcheck.py): exp(h) and dh bit-identical to the restatement, y, dx and
 dE within the FP32 summation bound of FP64 products.
 """
@@ -74,4 +74,25 @@ def test_every_token_of_the_mixing_workload():
     assert torch.equal(y2, y) and torch.equal(dh2, dh) and torch.equal(dx2, dx)
     report = mix_parity(h, x, g, y, e, dx, dh, de, threads=oracle.default_threads())
     print(f"[parity] hc {json.dumps(report)}", flush=True)
+    assert not check_mix(report), check_mix(report)
+
+
+def test_every_token_of_the_wide_mixing_workload():
+    """The 8-stream workload (16,384 tokens x 8 streams x 4,096 columns, BF16): exp(h) from the
+    P = 8 kernel in FP32, then the apply kernels.  Every token: E and dh bit-identical to the
+    restatement (dh = L(h^T, dE) on the kernel's dE), y, dx and dE within their summation bounds;
+    autograd through fh.mix_streams returns the kernels' results."""
+    import bench
+
+    h, x, g = bench.make_mix_inputs(torch, "cuda", shape=bench.MIX_WIDE_SHAPE)
+    ops = torch.ops.flash_hypercons
+    e = ops._matrix_exp(h.float())
+    y = fh.mix_streams(h, x)
+    assert torch.equal(y, ops._hc_apply(e, x))
+    dx, de = ops._hc_apply_backward(e, x, g)
+    hr, xr = h.clone().requires_grad_(), x.clone().requires_grad_()
+    dh, dx2 = torch.autograd.grad(fh.mix_streams(hr, xr), (hr, xr), g)
+    assert torch.equal(dx2, dx)
+    report = mix_parity(h, x, g, y, e, dx, dh, de, threads=oracle.default_threads())
+    print(f"[parity] hc8 {json.dumps(report)}", flush=True)
     assert not check_mix(report), check_mix(report)

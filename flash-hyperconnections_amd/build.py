@@ -67,6 +67,21 @@ HIP_FLAGS = [
 ]
 
 
+# Per-source additions.  expm_p4.hip (the VALU-bound P = 4 kernels) is scheduled for
+# instruction-level parallelism: against the default scheduler, same process, alternating, two
+# boxes: config 2 step -1.6% / -3.4% (forward -3% / -4%), config 3 step -1.7% / -2.2%, results
+# bit-identical.  The same strategy made the P = 16 tile Frechet kernel 3% slower and the fused
+# mixing backward 3% slower, so the other sources keep the default.
+SOURCE_FLAGS = {
+    "expm_p4.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
+}
+
+
+def hip_flags(src: str) -> list[str]:
+    """hipcc flags for one kernel source."""
+    return HIP_FLAGS + SOURCE_FLAGS.get(src, [])
+
+
 def _run(cmd: list[str]) -> None:
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     out = "\n".join(
@@ -79,7 +94,7 @@ def _run(cmd: list[str]) -> None:
 
 def _compile(src: str, obj_dir: Path = OBJ) -> Path:
     obj = obj_dir / (src + ".o")
-    _run([HIPCC, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+    _run([HIPCC, *hip_flags(src), "-c", str(CSRC / src), "-o", str(obj)])
     return obj
 
 

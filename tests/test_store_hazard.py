@@ -61,7 +61,7 @@ def test_scanner_flags_an_overwrite():
 
 
 def _assembly(source: str, out: Path) -> str:
-    flags = [f for f in fh_build.HIP_FLAGS if f != "-fPIC"]
+    flags = [f for f in fh_build.hip_flags(source) if f != "-fPIC"]
     proc = subprocess.run([fh_build.HIPCC, *flags, "--cuda-device-only", "-S", str(fh_build.CSRC / source), "-o",
                            str(out)], capture_output=True, text=True)
     assert proc.returncode == 0, f"{source}: {proc.stderr[-2000:]}"
@@ -83,23 +83,55 @@ def test_kernels_keep_store_data_until_read(assembly):
 
 
 KERNEL_SCRATCH = re.compile(r"\.amdhsa_kernel (\S+)\n(?:.*\n)*?\s*\.amdhsa_private_segment_fixed_size (\d+)")
+SPILL = re.compile(r"\bscratch_(store|load)|Folded (Spill|Reload)")
 
 # Kernels on the measured paths: the P = 4 dense (buffer-to-LDS) and count-ordered kernels, the
-# P = 8 and tile kernels, and the stream-mixing kernels.  Register spills there would add scratch
-# traffic to the HBM-bound launches.
+# P = 8 and tile kernels, and the stream-mixing kernels.  A register spill inside their loops
+# (where the per-group, per-matrix or per-token work runs) would add scratch traffic to every
+# unit of work; the mixing kernels, which stream at the HBM rate, keep no scratch at all.
 NO_SCRATCH = ("expm_p4_dma_kernel", "expm_p4_sort_kernel", "expm_oct_kernel", "expm_oct16", "expm_tile_kernel",
               "hc_mix_fwd_kernel", "hc_mix_bwd_kernel", "hc_wide_fwd_kernel", "hc_wide_bwd_kernel")
+NO_SCRATCH_AT_ALL = ("hc_mix_fwd_kernel", "hc_mix_bwd_kernel", "hc_wide_fwd_kernel", "hc_wide_bwd_kernel")
 
 
-def test_scanner_reads_scratch_sizes():
+def spills_in_loops(asm: str) -> dict[str, int]:
+    """Per function, the spill and reload instructions inside a loop: in blocks the compiler's
+    assembly annotates as a loop header or as in a loop."""
+    found = {}
+    for m in re.finditer(r"^(_Z\S+):", asm, re.M):
+        end = asm.find(".Lfunc_end", m.end())
+        in_loop, count = False, 0
+        for line in asm[m.end():end if end >= 0 else None].splitlines():
+            text = line.strip()
+            if text.startswith(".LBB") or text.startswith("; %bb."):
+                in_loop = "Loop" in text
+            elif in_loop and SPILL.search(text):
+                count += 1
+        if count:
+            found[m.group(1)] = count
+    return found
+
+
+def test_scanners_read_scratch_sizes_and_loop_spills():
     asm = ("\t.amdhsa_kernel _Zk1\n\t\t.amdhsa_group_segment_fixed_size 0\n\t\t.amdhsa_private_segment_fixed_size 64\n"
            "\t.amdhsa_kernel _Zk2\n\t\t.amdhsa_private_segment_fixed_size 0\n")
     assert KERNEL_SCRATCH.findall(asm) == [("_Zk1", "64"), ("_Zk2", "0")]
+    body = ("_Zk1:\n\tv_mov_b32 v0, 0\n.LBB0_2:  ; =>This Loop Header: Depth=1\n\tv_add_f32 v1, v2, v3\n"
+            "\tscratch_store_dword off, v4, off ; 4-byte Folded Spill\n; %bb.3:  ;   in Loop: Header=BB0_2 Depth=1\n"
+            "\tscratch_load_dword v4, off, off ; 4-byte Folded Reload\n; %bb.4:\n"
+            "\tscratch_store_dword off, v5, off ; 4-byte Folded Spill\n.Lfunc_end0:\n"
+            "_Zk2:\n; %bb.0:\n\tscratch_store_dword off, v5, off ; 4-byte Folded Spill\n.Lfunc_end1:\n")
+    assert spills_in_loops(body) == {"_Zk1": 2}
 
 
-def test_measured_kernels_use_no_scratch(assembly):
+def test_measured_kernels_spill_nothing_inside_loops(assembly):
     sizes = {name: int(size) for text in assembly.values() for name, size in KERNEL_SCRATCH.findall(text)}
     hot = {name: size for name, size in sizes.items() if any(k in name for k in NO_SCRATCH)}
     assert len(hot) > 60, sorted(hot)  # every instantiation of those kernels was found
-    spilling = {name: size for name, size in hot.items() if size}
-    assert not spilling, spilling
+    loops = {}
+    for text in assembly.values():
+        loops.update(spills_in_loops(text))
+    in_loops = {name: count for name, count in loops.items() if any(k in name for k in NO_SCRATCH)}
+    assert not in_loops, in_loops
+    streaming = {name: size for name, size in hot.items() if any(k in name for k in NO_SCRATCH_AT_ALL) and size}
+    assert not streaming, streaming

@@ -203,13 +203,15 @@ __device__ __forceinline__ PQ<Pair> comb(const PQ<Pair>& a, const PQ<Pair>& a2, 
   PQ<Pair> b;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
+    // c0 * I, with +0 from a VGPR where c0 is 0 (see vgpr_zero).
+    const float i0 = c0 != 0.f ? c0 * diag.v[r] : vgpr_zero();
     float t;
     if constexpr (c1 != 0.f) {
-      t = __builtin_fmaf(c1, a.d.v[r], c0 * diag.v[r]);
+      t = __builtin_fmaf(c1, a.d.v[r], i0);
+      t = __builtin_fmaf(c2, a2.d.v[r], t);
     } else {
-      t = c0 * diag.v[r];
+      t = __builtin_fmaf(c2, a2.d.v[r], i0);
     }
-    t = __builtin_fmaf(c2, a2.d.v[r], t);
     t = __builtin_fmaf(c3, a3.d.v[r], t);
     if constexpr (c6 != 0.f) t = __builtin_fmaf(c6, a6.d.v[r], t);
     b.d.v[r] = t;

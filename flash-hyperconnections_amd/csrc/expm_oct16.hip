@@ -131,14 +131,15 @@ __device__ __forceinline__ float comb_entry(int e, const O16& a, const O16& a2, 
                                             const float (&dq)[4]) {
   constexpr float c0 = kCoef[K][0], c1 = kCoef[K][1], c2 = kCoef[K][2], c3 = kCoef[K][3], c6 = kCoef[K][4];
   const int beta = e >> 2, r = e & 3;
-  const float i0 = (beta == 0 || beta == 3) ? c0 * dq[r] : 0.f;
+  // c0 * I, with +0 from a VGPR off the diagonal blocks and where c0 is 0 (see vgpr_zero).
+  const float i0 = c0 != 0.f && (beta == 0 || beta == 3) ? c0 * dq[r] : vgpr_zero();
   float t;
   if constexpr (c1 != 0.f) {
     t = __builtin_fmaf(c1, a.v[e], i0);
+    t = __builtin_fmaf(c2, a2.v[e], t);
   } else {
-    t = i0;
+    t = __builtin_fmaf(c2, a2.v[e], i0);
   }
-  t = __builtin_fmaf(c2, a2.v[e], t);
   t = __builtin_fmaf(c3, a3.v[e], t);
   if constexpr (c6 != 0.f) t = __builtin_fmaf(c6, a6.v[e], t);
   return t;

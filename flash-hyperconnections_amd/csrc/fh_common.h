@@ -29,6 +29,20 @@ constexpr double kTheta18 = 3.010066362817634;
 
 __device__ constexpr float kCoef[5][5] = FH_COEF_TABLE;
 
+// +0 held in a VGPR the compiler cannot see through.  A combine's first term
+// fmaf(c, x, +0) with the +0 constant-folded has to take the coefficient from
+// an SGPR (gfx9's three-operand encoding carries no literal); with +0 in a
+// VGPR it encodes as v_fmamk_f32 with the coefficient as a literal, same
+// operation, same bits.  In isolation gfx950 issues the SGPR form ~1.6x
+// slower (4.7 against 2.9 cycles per instruction at two wavefronts per SIMD);
+// in the P = 8 forward kernel the literal form measured 5% faster, in the
+// P = 4 and tile kernels no faster, which keep the SGPR form.
+__device__ __forceinline__ float vgpr_zero() {
+  float z;
+  asm("v_mov_b32 %0, 0" : "=v"(z));
+  return z;
+}
+
 // Element types, tagged by the reference's dtype codes
 // (csrc/matrix_exp.cu:17: 0 = float32, 1 = bfloat16, 2 = float16).
 struct F32 {

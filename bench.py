@@ -77,9 +77,10 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def make_inputs(name: str, torch, device):
-    """Seeded synthetic inputs per BASELINE configs 2-5 (seed 0; base, then per-matrix scale, then grad)."""
-    torch.manual_seed(0)
+def make_inputs(name: str, torch, device, seed: int = 0):
+    """Seeded synthetic inputs per BASELINE configs 2-5 (seed 0 unless given; base, then per-matrix
+    scale, then grad)."""
+    torch.manual_seed(seed)
     if name == "c2":
         b, n = 1 << 20, 4
         x = torch.randn(b, n, n) * 0.25
@@ -565,8 +566,9 @@ def cpu_leg(torch, kept: dict, mix_kept: dict | None = None) -> dict:
             failures[name] = why
     result["parity"] = {"pass": not failures, "failures": failures, "configs": parity,
                         "rule": "tests/fullsize.py check(): s == oracle for every matrix; n <= 8 bit-identical "
-                        "to the oracle; strict north-star failures <= the oracle's; FP32 mean error <= 1.05x "
-                        "the oracle's; per-matrix excess over the oracle's error under a sanity cap. hc, hc8 "
+                        "to the oracle; n >= 9: strict north-star failures <= the oracle's + 3 sqrt(oracle's) "
+                        "+ 3 and mean error <= 1.05x the oracle's; per-matrix excess over the oracle's error "
+                        "under a sanity cap. hc, hc8 "
                         "(tests/mixcheck.py): exp(h) and dh bit-identical to the oracle, y / dx / dE within "
                         "the FP32 summation bound of the FP64 products, every token"}
     return result

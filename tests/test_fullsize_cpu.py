@@ -11,7 +11,8 @@ import pytest
 import torch
 
 import oracle
-from tests.fullsize import direction_parity, error_ratio, excess_over_reference, strict_failures
+from tests.fullsize import (direction_parity, error_ratio, excess_over_reference, strict_failure_allowance,
+                            strict_failures)
 from tests.reference import reference
 
 
@@ -99,10 +100,21 @@ def test_overflow_band_and_gate():
             "max_excess_over_reference": 1.2, "excess_unit": "ratio", "debug_launch_matches_op": True}
     assert check(good, 32) == [] and check(good, 4) == []
     for key, value, n in (("s_mismatches", 1, 32), ("bitwise_mismatches_vs_oracle", 5, 4),
-                          ("strict_failures_kernel", 4, 32), ("mean_rel_frobenius", 1.2e-6, 32),
-                          ("max_excess_over_reference", 5.0, 32), ("debug_launch_matches_op", False, 32)):
+                          ("strict_failures_kernel", 4, 4), ("strict_failures_kernel", 12, 32),
+                          ("mean_rel_frobenius", 1.2e-6, 32), ("max_excess_over_reference", 5.0, 32),
+                          ("debug_launch_matches_op", False, 32)):
         assert check({**good, key: value}, n), key
     assert check({**good, "bitwise_mismatches_vs_oracle": 7}, 32) == []  # n >= 16 need not match in bits
+    # Tiles: binomial noise on the count is allowed (3 + 3 sqrt(3) + 3 = 11), none at n <= 8.
+    assert strict_failure_allowance(3) == 8 and strict_failure_allowance(500) == 70
+    assert check({**good, "strict_failures_kernel": 11}, 32) == []
+    # FP16/BF16: the mean normwise error, in output ulps, against the restatement's.
+    low = {**good, "excess_unit": "output ulps", "max_excess_over_reference": -1.0, "mean_normwise_ulps": 1.0e-4,
+           "oracle_mean_normwise_ulps": 1.0e-4}
+    del low["mean_rel_frobenius"], low["oracle_mean_rel_frobenius"]
+    assert check(low, 32) == []
+    assert check({**low, "mean_normwise_ulps": 1.1e-4}, 32)
+    assert check({**low, "max_excess_over_reference": 2.5}, 32)
 
 
 def test_normwise_floor_uses_overflowed_scale():

@@ -290,12 +290,12 @@ def measure_config(name: str, torch, fh, steps: int, warmup: int, trials: int, d
 MIX_SHAPE = (16384, 4, 4096)  # tokens, streams, columns
 
 
-def make_mix_inputs(torch, device, shape=MIX_SHAPE, dtype=None):
+def make_mix_inputs(torch, device, shape=MIX_SHAPE, dtype=None, seed: int = 0):
     """Seeded inputs of the fused stream mixing: per token an n x n generator h ~ N(0, 0.25^2)
     (config 2's law) and n residual streams x ~ N(0, 1) of width C; upstream gradient N(0, 1)."""
     dtype = dtype or torch.bfloat16
     tokens, n, cols = shape
-    gen = torch.Generator(device=device).manual_seed(0)
+    gen = torch.Generator(device=device).manual_seed(seed)
     h = (torch.randn(tokens, n, n, device=device, generator=gen) * 0.25).to(dtype)
     x = torch.randn(tokens, n, cols, device=device, generator=gen).to(dtype)
     g = torch.randn(tokens, n, cols, device=device, generator=gen).to(dtype)

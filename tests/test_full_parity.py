@@ -67,10 +67,11 @@ def test_every_matrix_of_baseline_config(name, seed):
         assert report["forward"]["strict_failures_oracle"] > 0
 
 
-def test_every_token_of_the_mixing_workload():
+@pytest.mark.parametrize("seed", [0, 1])
+def test_every_token_of_the_mixing_workload(seed):
     import bench
 
-    h, x, g = bench.make_mix_inputs(torch, "cuda")
+    h, x, g = bench.make_mix_inputs(torch, "cuda", seed=seed)
     ops = torch.ops.flash_hypercons
     y, _, e = ops._hc_mix_aux(h, x, None)
     dx, dh, de = ops._hc_mix_aux(h, x, g)
@@ -79,18 +80,19 @@ def test_every_token_of_the_mixing_workload():
     dh2, dx2 = torch.autograd.grad(y2, (hr, xr), g)
     assert torch.equal(y2, y) and torch.equal(dh2, dh) and torch.equal(dx2, dx)
     report = mix_parity(h, x, g, y, e, dx, dh, de, threads=oracle.default_threads())
-    print(f"[parity] hc {json.dumps(report)}", flush=True)
+    print(f"[parity] hc seed {seed} {json.dumps(report)}", flush=True)
     assert not check_mix(report), check_mix(report)
 
 
-def test_every_token_of_the_wide_mixing_workload():
+@pytest.mark.parametrize("seed", [0, 1])
+def test_every_token_of_the_wide_mixing_workload(seed):
     """The 8-stream workload (16,384 tokens x 8 streams x 4,096 columns, BF16): exp(h) from the
     P = 8 kernel in FP32, then the apply kernels.  Every token: E and dh bit-identical to the
     restatement (dh = L(h^T, dE) on the kernel's dE), y, dx and dE within their summation bounds;
     autograd through fh.mix_streams returns the kernels' results."""
     import bench
 
-    h, x, g = bench.make_mix_inputs(torch, "cuda", shape=bench.MIX_WIDE_SHAPE)
+    h, x, g = bench.make_mix_inputs(torch, "cuda", shape=bench.MIX_WIDE_SHAPE, seed=seed)
     ops = torch.ops.flash_hypercons
     e = ops._matrix_exp(h.float())
     y = fh.mix_streams(h, x)
@@ -100,5 +102,5 @@ def test_every_token_of_the_wide_mixing_workload():
     dh, dx2 = torch.autograd.grad(fh.mix_streams(hr, xr), (hr, xr), g)
     assert torch.equal(dx2, dx)
     report = mix_parity(h, x, g, y, e, dx, dh, de, threads=oracle.default_threads())
-    print(f"[parity] hc8 {json.dumps(report)}", flush=True)
+    print(f"[parity] hc8 seed {seed} {json.dumps(report)}", flush=True)
     assert not check_mix(report), check_mix(report)

@@ -176,3 +176,34 @@ def test_package_under_test():
     assert in_tree != (os.environ.get("FH_TEST_INSTALLED", "") not in ("", "0"))
     assert (pkg / "libflash_hypercons_hip.so").is_file() and (pkg / "_C.so").is_file()
     assert Path(flash_hypercons._C.__file__).resolve().parent == pkg
+
+
+def test_last_error_is_per_thread():
+    """fh_last_error() reports the last failing call of the calling thread only."""
+    import threading
+
+    lib = load()
+    lib.fh_last_error.restype = ctypes.c_char_p
+    lib.fh_matrix_exp.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
+                                  ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
+    strides = (ctypes.c_int64 * 3)(16, 4, 1)
+    failed = threading.Event()
+    seen = {}
+
+    def failing():
+        seen["rc"] = lib.fh_matrix_exp(None, strides, 0, None, 0, 4, 33, None)
+        seen["failing"] = lib.fh_last_error()
+        failed.set()
+
+    def clean():
+        failed.wait(10)
+        seen["ok_rc"] = lib.fh_matrix_exp(None, strides, 0, None, 0, 0, 4, None)  # empty batch: succeeds
+        seen["clean"] = lib.fh_last_error()
+
+    threads = [threading.Thread(target=failing), threading.Thread(target=clean)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(10)
+    assert seen["rc"] == 1 and b"2 <= N <= 32" in seen["failing"]
+    assert seen["ok_rc"] == 0 and seen["clean"] == b""

@@ -144,32 +144,43 @@ def test_normwise_reads_infinity_as_an_interval():
 
 def test_sweep_overflow_rule_on_planted_results():
     """The seeded sweep's rule for n >= 9 results the reference arithmetic overflows
-    (tests/test_parity_sweep.py::_mismatches), on a stand-in result made from the oracle: where
-    the oracle holds +-inf or NaN, a non-finite value of either kind or a finite one at the top of
-    the output range passes; an ordinary finite value fails, and so does a NaN where the oracle's
-    result is finite."""
+    (tests/test_parity_sweep.py::_mismatches), on a stand-in result made from the oracle and
+    judged against the FP64 exact result: where the exact value lies beyond the output range, a
+    non-finite value of either kind or a finite one at the top of the range passes and an ordinary
+    finite value fails; where it lies within the range, a non-finite value or one within the
+    tolerance passes and one far off fails; a NaN where the oracle's result is finite fails."""
+    from tests.reference import reference
     from tests.test_parity_sweep import _mismatches
 
     n, dtype = 10, torch.bfloat16
-    x = torch.eye(n, dtype=torch.float64).repeat(2, 1, 1) * torch.tensor([0.1, 100.0])[:, None, None]
-    x[1, 0, 1:] = 100.0  # exp(100) ~ 2.7e43: the exact exponential lies beyond the BF16/FP32 range
+    # exp(89 I) = e^89 I: its diagonal (4.5e38) lies just beyond the BF16/FP32 range, its zeros inside.
+    x = torch.eye(n, dtype=torch.float64).repeat(2, 1, 1) * torch.tensor([0.1, 89.0])[:, None, None]
     x = x.to(dtype)
     want, want_s = oracle.torch_matrix_exp(x)
     assert bool(torch.isfinite(want[0]).all()) and not bool(torch.isfinite(want[1]).all())
-    bad = (~torch.isfinite(want[1])).nonzero()[0].tolist()
+    exact = lambda rows: reference(x[rows])  # noqa: E731
+    ex1 = reference(x[1:2])[0]
     top = torch.finfo(dtype).max
+    bad = ((~torch.isfinite(want[1])) & (ex1.abs() > top)).nonzero()[0].tolist()
+    inside = (ex1.abs() < top).nonzero()[0].tolist()
 
-    def planted(value):
+    def planted(value, at):
         out = want.clone()
-        out[1, bad[0], bad[1]] = value
+        out[1, at[0], at[1]] = value
         return out
 
-    assert _mismatches(want, want_s, want, want_s, n, dtype) == []
+    def rule(out):
+        return _mismatches(out, want_s, want, want_s, n, dtype, exact)
+
+    assert rule(want) == []
     other = float("nan") if not bool(want[1, bad[0], bad[1]].isnan()) else float("inf")
-    assert _mismatches(planted(other), want_s, want, want_s, n, dtype) == []
-    assert _mismatches(planted(0.99 * top), want_s, want, want_s, n, dtype) == []
-    assert _mismatches(planted(1.0), want_s, want, want_s, n, dtype)
-    assert _mismatches(planted(-0.5 * top), want_s, want, want_s, n, dtype)
+    assert rule(planted(other, bad)) == []
+    assert rule(planted(0.99 * top, bad)) == []
+    assert rule(planted(1.0, bad))
+    assert rule(planted(-0.5 * top, bad))
+    assert rule(planted(float("inf"), inside)) == []  # the kernel's own order may overflow
+    assert rule(planted(0.0, inside)) == []
+    assert rule(planted(0.9 * top, inside))
     out = want.clone()
     out[0, 2, 3] = float("nan")
-    assert _mismatches(out, want_s, want, want_s, n, dtype)
+    assert rule(out)

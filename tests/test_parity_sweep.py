@@ -12,16 +12,20 @@ stride-0 batch), the direction (forward, or Frechet with its own layout) and the
   oracle entry, and no NaN, wherever the oracle's result is finite.
 
 The rule for an n >= 9 result the reference's arithmetic overflows (its exact value reaches
-the top of the output type's range: 1-norms of several hundred, s = 6 and up): every element
-the oracle holds as non-finite is, in the kernel's result, either non-finite too or finite at
-the top of the range (|y| >= (1 - tol) * the type's maximum, tol as above), so an overflow is
-never reported as an ordinary finite number.  Whether such an element is NaN (inf - inf inside
-a sum) or +-inf, and whether an element whose exact value sits at the range's top rounds to
-infinity or to the largest finite values, depends on the order of each sum's terms, which the
-MFMA tiles do not share with the reference; those are not compared.  Four cases of earlier
-3000-case sweeps are kept as fixed regression cases: two where the kernel holds +-inf and the
-oracle NaN, two where the kernel holds a finite value at the top of the range (BF16 exact
-values of 3.24e38-3.39e38, FP16 65520.3) and the oracle's own order overflowed.
+the top of the output type's range: 1-norms of several hundred, s = 6 and up) compares the
+kernel with the FP64 exact result, element by element: where the exact value lies beyond the
+output range, the kernel's element is non-finite or finite at the top of the range
+(|y| >= (1 - tol) * the type's maximum, tol as above), so an overflow is never reported as an
+ordinary finite number; where it lies within the range, the kernel's element is non-finite
+(its own order overflowed) or within tol of the matrix's largest exact entry.  The reference's
+own order can return +-inf, even of the wrong sign, for elements whose exact value is finite.
+Whether an element is NaN (inf - inf inside a sum) or +-inf, and whether an element whose exact
+value sits at the range's top rounds to infinity or to the largest finite values, depends on the
+order of each sum's terms, which the MFMA tiles do not share with the reference; those are not
+compared.  Five cases of earlier 3000-case sweeps are kept as fixed regression cases: two where
+the kernel holds +-inf and the oracle NaN, two where the kernel holds a finite value at the top
+of the range (BF16 exact values of 3.24e38-3.39e38, FP16 65520.3) and the oracle's own order
+overflowed, one where the oracle's order overflowed elements whose exact values are finite.
 """
 
 import math
